@@ -1,0 +1,143 @@
+"""CPU oracle of the W8A8 SmoothQuant linear path: TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import this package, and only as the checker
+(or, for the baseline, as the timed CPU restatement).  The product package (vllm_turing_amd) never imports it.
+
+The arithmetic lives in w8a8_oracle.c (plain C, IEEE float32, no contraction), built by oracle/Makefile into
+oracle/build/liboracle.so.  This module wraps it with numpy arrays.  Each wrapper names the reference lines it
+restates; w8a8_oracle.c states how each function is pinned.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "build", "liboracle.so")
+_lib = None
+
+FP16, BF16 = 0, 1
+ORDER_SMALL_M, ORDER_LARGE_M = 0, 1
+
+
+def build():
+    """Compile the C restatement (make in oracle/)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_SO):
+            raise RuntimeError(f"oracle library missing: {_SO} (run `make -C oracle`)")
+        L = ctypes.CDLL(_SO)
+        vp, lg, i = ctypes.c_void_p, ctypes.c_long, ctypes.c_int
+        L.o_quant_rows.argtypes = [vp, i, lg, lg, lg, vp, vp]
+        L.o_gemm_i32.argtypes = [vp, vp, vp, lg, lg, lg]
+        L.o_gemm_i32.restype = i
+        L.o_epilogue.argtypes = [vp, vp, vp, vp, vp, lg, lg, i, i, i, i]
+        L.o_silu_h.argtypes = [ctypes.c_uint16, i]
+        L.o_silu_h.restype = ctypes.c_uint16
+        L.o_silu_table.argtypes = [i, vp]
+        L.o_silu_mul_quant.argtypes = [vp, i, lg, lg, vp, vp, vp]
+        L.o_h2f.argtypes = [ctypes.c_uint16]
+        L.o_h2f.restype = ctypes.c_float
+        L.o_f2h.argtypes = [ctypes.c_float]
+        L.o_f2h.restype = ctypes.c_uint16
+        L.o_bf2f.argtypes = [ctypes.c_uint16]
+        L.o_bf2f.restype = ctypes.c_float
+        L.o_f2bf.argtypes = [ctypes.c_float]
+        L.o_f2bf.restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _bits(x):
+    """fp16 / bf16 data as uint16 bit patterns (numpy uint16 array) plus its dtype code."""
+    if hasattr(x, "dtype") and str(x.dtype) in ("torch.float16", "torch.bfloat16"):
+        import torch
+        code = FP16 if x.dtype == torch.float16 else BF16
+        return np.ascontiguousarray(x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)), code
+    if isinstance(x, np.ndarray) and x.dtype == np.float16:
+        return np.ascontiguousarray(x.view(np.uint16)), FP16
+    raise TypeError("expected fp16/bf16 torch tensor or fp16 numpy array")
+
+
+def quant_rows(x):
+    """Per-token dynamic int8 quant (quantfuse.py:18-24, zero-row rule silu_quant.cu:57-58).
+
+    x: [M, K] fp16/bf16 (torch or numpy fp16) -> (q int8 [M, K], s float32 [M])."""
+    xb, code = _bits(x)
+    M, K = xb.shape
+    q = np.empty((M, K), np.int8)
+    s = np.empty(M, np.float32)
+    lib().o_quant_rows(_p(xb), code, M, K, K, _p(q), _p(s))
+    return q, s
+
+
+def gemm_i32(a, w):
+    """acc[m, n] = sum_k a[m, k] w[n, k] in exact integer arithmetic (w8a8_gemv.cu:53-81, w8a8_big.cu:36-43)."""
+    a = np.ascontiguousarray(a, np.int8)
+    w = np.ascontiguousarray(w, np.int8)
+    M, K = a.shape
+    N = w.shape[0]
+    acc = np.empty((M, N), np.int32)
+    if lib().o_gemm_i32(_p(a), _p(w), _p(acc), M, N, K) != 0:
+        raise ValueError("K too large for exact int32 accumulation")
+    return acc
+
+
+def epilogue(acc, sa, sw, bias=None, dtype=FP16, order=ORDER_SMALL_M):
+    """Scale epilogue (order 0: w8a8_gemv.cu:87-91; order 1: w8a8_big.cu:26-35).
+
+    acc int32 [M, N]; sa float32 [M] or [1]; sw float32 [N] or [1]; bias uint16 bits [N] or None.
+    Returns uint16 bit patterns [M, N] of fp16 (dtype 0) or bf16 (dtype 1)."""
+    acc = np.ascontiguousarray(acc, np.int32)
+    sa = np.ascontiguousarray(np.asarray(sa, np.float32).reshape(-1))
+    sw = np.ascontiguousarray(np.asarray(sw, np.float32).reshape(-1))
+    M, N = acc.shape
+    out = np.empty((M, N), np.uint16)
+    b = None if bias is None else np.ascontiguousarray(np.asarray(bias, np.uint16).reshape(-1))
+    lib().o_epilogue(_p(acc), _p(sa), _p(sw), None if b is None else _p(b), _p(out), M, N,
+                     int(sa.size > 1), int(sw.size > 1), dtype, order)
+    return out
+
+
+def silu_h(x_bits, dtype=FP16):
+    """silu of one fp16/bf16 bit pattern (silu_quant.cu:11-14) -> bit pattern."""
+    return lib().o_silu_h(int(x_bits), dtype)
+
+
+def silu_table(dtype=FP16):
+    """All 65,536 silu_h outputs of one type, indexed by input bit pattern."""
+    t = np.empty(65536, np.uint16)
+    lib().o_silu_table(dtype, _p(t))
+    return t
+
+
+def silu_mul_quant(gu):
+    """SiLU(gate) * up + per-row int8 quant (silu_quant.cu:22-69).
+
+    gu: [M, 2I] fp16/bf16 -> (q int8 [M, I], s float32 [M], act bit patterns uint16 [M, I])."""
+    gb, code = _bits(gu)
+    M, I2 = gb.shape
+    I = I2 // 2
+    q = np.empty((M, I), np.int8)
+    s = np.empty(M, np.float32)
+    act = np.empty((M, I), np.uint16)
+    lib().o_silu_mul_quant(_p(gb), code, M, I, _p(q), _p(s), _p(act))
+    return q, s, act
+
+
+def scaled_mm(a_q, w_q, sa, sw, bias=None, dtype=FP16, order=None):
+    """The whole scaled int8 matmul: acc = a_q . w_q^T, then the epilogue of the reference path that M takes
+    (order 0 for M <= 32, the GEMV / MMA kernels; order 1 above, w8a8.py:108-117 dispatch)."""
+    acc = gemm_i32(a_q, w_q)
+    if order is None:
+        order = ORDER_SMALL_M if acc.shape[0] <= 32 else ORDER_LARGE_M
+    return epilogue(acc, sa, sw, bias, dtype, order), acc
