@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 linear path on one MI355X.
+
+Headline (the `value`): decode GEMV at M=1, K=5120, N=17408 (int8 weights, per-token activation scale, per-channel
+weight scale, fp16 out), in GB/s of algorithmic bytes N*K + M*K + 2*M*N + 4*N + 4*M per launch.  One step is one
+GEMV launch.  Five weight copies (445 MB) are rotated so the 256 MB Infinity Cache cannot hold them: the weights
+stream from HBM.  Launches are captured in a HIP graph of 20 back-to-back launches and replayed, so the timed region
+is GPU work only (HIP events on the launch stream, bracketed by synchronizations).
+
+Also reported:
+  gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline);
+  quant: per-token quant at M=4096, K=5120 and SiLU*up+quant at M=4096, I=17408, in GB/s (HBM-bound);
+  cpu_baseline: the reference's CPU path restated (oracle/cpu_path.py: torch CPU int8 matmul + dequant), timed on a
+    bounded sample on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "W8A8 GEMM TOPS @M=4096 + GEMV HBM GB/s @M=1 (1×MI355X, % roofline)"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+
+
+def traffic_from_profiles(key):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel
+    calibration), as recorded in profiles/*.md lines `traffic[<key>] = <bytes> bytes/launch`."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    pat = re.compile(r"traffic\[" + re.escape(key) + r"\]\s*=\s*([0-9.eE+]+)\s*bytes/launch")
+    for f in sorted(os.listdir(pdir)):
+        if f.endswith((".md", ".txt")):
+            m = pat.search(open(os.path.join(pdir, f)).read())
+            if m:
+                return float(m.group(1))
+    return None
+
+
+def graph_time(torch, launch, n_launch_per_graph, steps, warmup):
+    """Capture n launches in a HIP graph, replay; return ms per launch over `steps` launches."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n_launch_per_graph):          # warm up outside capture (loads the code object)
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_launch_per_graph):
+            launch(i)
+    reps_w = max(1, warmup // n_launch_per_graph)
+    reps = max(1, (steps + n_launch_per_graph - 1) // n_launch_per_graph)
+    for _ in range(reps_w):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return ms / (reps * n_launch_per_graph), reps * n_launch_per_graph
+
+
+def cpu_time(fn, budget_s):
+    """Median seconds per call of fn over calls fitting in ~budget_s (at least 3, after one warm-up call)."""
+    fn()
+    ts = []
+    t_end = time.time() + budget_s
+    while len(ts) < 3 or (time.time() < t_end and len(ts) < 50):
+        t = time.time()
+        fn()
+        ts.append(time.time() - t)
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this W8A8 path has no multi-GPU mode (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vllm_turing_amd import _lib, workloads
+    from vllm_turing_amd.quantfuse import per_token_quant
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    L = _lib.lib()
+    st = lambda: torch.cuda.current_stream().cuda_stream
+    result = {}
+
+    # ---- decode GEMV, M=1 -----------------------------------------------------------------------------------------
+    M, K, N = 1, workloads.HIDDEN, workloads.INTERMEDIATE
+    copies = 5
+    c = workloads.decode(M)
+    x_q, x_s = per_token_quant(c["x"].to(dev))
+    gw = torch.Generator(device=dev).manual_seed(1)
+    ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gw) for _ in range(copies)]
+    sw = c["sw"].to(dev)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+
+    def gemv(i):
+        rc = L.w8a8_gemv(x_q.data_ptr(), ws[i % copies].data_ptr(), x_s.data_ptr(), sw.data_ptr(), None,
+                         out.data_ptr(), M, N, K, 1, 1, 0, st())
+        if rc != 0:
+            raise RuntimeError(f"w8a8_gemv {rc}")
+
+    print(f"[bench] GEMV M={M} K={K} N={N}, {copies} weight copies", file=sys.stderr, flush=True)
+    ms_gemv, n_gemv = graph_time(torch, gemv, 4 * copies, args.steps, args.warmup)
+    gemv_bytes = N * K + M * K + 2 * M * N + 4 * N + 4 * M
+    gemv_gbs = gemv_bytes / (ms_gemv * 1e-3) / 1e9
+    print(f"[bench] GEMV {ms_gemv * 1e3:.2f} us/launch, {gemv_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    del ws
+
+    # ---- prefill GEMM, M=4096, bias, bf16 ---------------------------------------------------------------------------
+    Mg, Kg, Ng = 4096, workloads.HIDDEN, 12288
+    p = workloads.prefill(Mg)
+    a_q, a_s = per_token_quant(p["x"].to(dev))
+    wg = p["w"].to(dev)
+    swg = p["sw"].to(dev)
+    bias = p["bias"].to(dev)
+    outg = torch.empty(Mg, Ng, dtype=torch.bfloat16, device=dev)
+
+    def gemm(i):
+        rc = L.w8a8_scaled_mm(a_q.data_ptr(), wg.data_ptr(), a_s.data_ptr(), swg.data_ptr(), bias.data_ptr(),
+                              outg.data_ptr(), Mg, Ng, Kg, 1, 1, 1, st())
+        if rc != 0:
+            raise RuntimeError(f"w8a8_scaled_mm {rc}")
+
+    print(f"[bench] GEMM M={Mg} K={Kg} N={Ng}", file=sys.stderr, flush=True)
+    gemm_steps = max(20, args.steps // 20)
+    ms_gemm, n_gemm = graph_time(torch, gemm, 4, gemm_steps, max(4, args.warmup // 20))
+    gemm_ops = 2.0 * Mg * Ng * Kg
+    gemm_tops = gemm_ops / (ms_gemm * 1e-3) / 1e12
+    print(f"[bench] GEMM {ms_gemm * 1e3:.1f} us/launch, {gemm_tops:.0f} TOPS", file=sys.stderr, flush=True)
+
+    # ---- quant kernels ------------------------------------------------------------------------------------------------
+    xq_in = torch.randn(Mg, Kg, dtype=torch.bfloat16, device=dev)
+    qq = torch.empty(Mg, Kg, dtype=torch.int8, device=dev)
+    sq = torch.empty(Mg, dtype=torch.float32, device=dev)
+
+    def quant(i):
+        rc = L.per_token_quant(xq_in.data_ptr(), qq.data_ptr(), sq.data_ptr(), Mg, Kg, Kg, 1, st())
+        if rc != 0:
+            raise RuntimeError(f"per_token_quant {rc}")
+
+    ms_q, _ = graph_time(torch, quant, 10, 200, 20)
+    quant_bytes = 3 * Mg * Kg + 4 * Mg
+    I = workloads.INTERMEDIATE
+    gu = torch.randn(Mg, 2 * I, dtype=torch.bfloat16, device=dev)
+    qs = torch.empty(Mg, I, dtype=torch.int8, device=dev)
+    ss = torch.empty(Mg, dtype=torch.float32, device=dev)
+
+    def smq(i):
+        rc = L.silu_mul_quant_bf16(gu.data_ptr(), qs.data_ptr(), ss.data_ptr(), Mg, I, st())
+        if rc != 0:
+            raise RuntimeError(f"silu_mul_quant {rc}")
+
+    ms_s, _ = graph_time(torch, smq, 4, 40, 8)
+    smq_bytes = 2 * Mg * 2 * I + Mg * I + 4 * Mg
+    print(f"[bench] quant {ms_q * 1e3:.1f} us, silu_mul_quant {ms_s * 1e3:.1f} us", file=sys.stderr, flush=True)
+
+    # ---- CPU baseline: the reference's CPU path (torch int8 matmul + dequant), bounded sample ---------------------
+    cpu = None
+    cpu_gemm = None
+    if not args.no_cpu:
+        from oracle import cpu_path
+        threads = torch.get_num_threads()
+        xc, wc, swc = c["x"], c["w"], c["sw"]
+        t_gemv, n_cpu = cpu_time(lambda: cpu_path.linear(xc, wc, swc, None, torch.float16), 10.0)
+        cpu = {"value": round(gemv_bytes / t_gemv / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"M=1 K={K} N={N} quant+int_mm+dequant, {n_cpu} calls, median"}
+        Ms = 256
+        xs_ = p["x"][:Ms]
+        t_g, n_g = cpu_time(lambda: cpu_path.linear(xs_, p["w"], p["sw"], p["bias"], torch.bfloat16), 10.0)
+        cpu_gemm = {"value": round(2.0 * Ms * Ng * Kg / t_g / 1e12, 3), "unit": "TOPS", "cores": threads,
+                    "kind": "port", "sample": f"M={Ms} of 4096 rows, K={Kg} N={Ng}, {n_g} calls, median"}
+        print(f"[bench] CPU GEMV {cpu['value']} GB/s, GEMM {cpu_gemm['value']} TOPS on {threads} threads",
+              file=sys.stderr, flush=True)
+
+    result = {
+        "metric": METRIC,
+        "value": round(gemv_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": n_gemv,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_gemv, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"decode W8A8 GEMV M={M} K={K} N={N} (int8 weights, fp16 out), {copies} rotated "
+                               f"weight copies ({copies * N * K / 1e6:.0f} MB > 256 MB MALL), HIP-graph replay",
+                   "M": M, "K": K, "N": N, "weight_copies": copies},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_m1")},
+        "cpu_baseline": cpu,
+        "gemm": {"workload": f"prefill W8A8 GEMM M={Mg} K={Kg} N={Ng}, bias, bf16 out", "ms": round(ms_gemm, 4),
+                 "launches": n_gemm, "tops": round(gemm_tops, 1),
+                 "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS,
+                              "unit": "TOPS", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+                              "traffic": traffic_from_profiles("gemm_m4096")},
+                 "cpu_baseline": cpu_gemm},
+        "quant": {"per_token_quant_M4096_K5120": {"us": round(ms_q * 1e3, 2),
+                                                   "gbs": round(quant_bytes / (ms_q * 1e-3) / 1e9, 1)},
+                  "silu_mul_quant_M4096_I17408": {"us": round(ms_s * 1e3, 2),
+                                                   "gbs": round(smq_bytes / (ms_s * 1e-3) / 1e9, 1)}},
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

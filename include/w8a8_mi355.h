@@ -1,0 +1,73 @@
+/*
+ * C ABI of the MI355X (gfx950) W8A8 SmoothQuant linear path: libw8a8_mi355.so.
+ *
+ * Plain pointers and sizes only.  Every buffer is allocated by the caller (torch tensors on the Python side); no entry
+ * point allocates, synchronizes or keeps state, so every launch is asynchronous on `stream` (a hipStream_t, e.g.
+ * torch.cuda.current_stream().cuda_stream) and can be captured in a HIP graph.  Argument validation happens before any
+ * HIP call and returns the documented code.
+ *
+ * dtype: 0 = float16, 1 = bfloat16 (activations, bias and output).  Weights are int8 [N, K] row-major (the layout vLLM
+ * stores; its cutlass_scaled_mm receives the [K, N] stride-(1, K) view of it).  Scales are float32: sa [M] (sa_rows=1)
+ * or [1] (per-tensor), sw [N] (sw_rows=1) or [1].  All int8 operands must be 16-byte aligned with K % 16 == 0.
+ */
+#ifndef W8A8_MI355_H
+#define W8A8_MI355_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Small-M W8A8 GEMV, M in [1, 16]: out[m, n] = T(fma(float(acc) * sa[m], sw[n], bias[n] or 0)).
+ * Replaces vllm_turing/csrc/w8a8_gemv.cu:347 (same arguments).  Returns -1 on bad arguments, else the HIP error code
+ * of the launch (0 = success). */
+int w8a8_gemv(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out, int M, int N,
+              int K, int sa_rows, int sw_rows, int dtype, void* stream);
+
+/* Small-M W8A8 GEMM, M in [1, 32], same arithmetic as w8a8_gemv.
+ * Replaces vllm_turing/csrc/w8a8_gemv.cu:330 (same arguments and return codes). */
+int w8a8_mma(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out, int M, int N,
+             int K, int sa_rows, int sw_rows, int dtype, void* stream);
+
+/* Prefill W8A8 GEMM, any M (dispatched for M > 32), per-row sa [M] and per-column sw [N], no bias, N % 16 == 0:
+ * out[m, n] = T(sa[m] * float(float(acc) * sw[n])).
+ * Replaces vllm_turing/csrc/w8a8_big.cu:66 (same arguments).  Returns 0 ok, 1 cannot implement (shape, alignment),
+ * 3 launch failed. */
+int w8a8_big(const void* A, const void* W, const void* sa, const void* sw, void* out, int M, int N, int K, int dtype,
+             void* stream);
+
+/* General scaled int8 matmul, any M, optional bias, per-row or per-tensor scales, with the large-M epilogue
+ * out = T(sa * float(float(acc) * sw)) or, with a bias, T(fma(sa, float(float(acc) * sw), bias)).
+ * Replaces the vLLM torch.ops._C.cutlass_scaled_mm fallback the reference calls at vllm_turing/w8a8.py:117 (same
+ * operands as w8a8_gemv).  Returns -1 on bad arguments, else the HIP error code of the launch. */
+int w8a8_scaled_mm(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out, int M,
+                   int N, int K, int sa_rows, int sw_rows, int dtype, void* stream);
+
+/* Dynamic symmetric per-token int8 quantization: scales[m] = absmax_m / 127,
+ * q[m, k] = clamp(rint(float(x[m, k]) * (127 / absmax_m)), -128, 127); a zero row gives q = 0 and scale 0.
+ * x: [M, K] fp16/bf16 with row stride ldx elements; q: [M, K] int8 contiguous; scales: [M] float32.
+ * Replaces the eager vllm._custom_ops.scaled_int8_quant(input, None, None, True) that
+ * vllm_turing/quantfuse.py:35-39 leaves to vLLM.  Returns 0, -1 on bad arguments, or the HIP launch error. */
+int per_token_quant(const void* x, void* q, void* scales, int M, int K, long ldx, int dtype, void* stream);
+
+/* SiLU(gate) * up + per-row dynamic int8 quantization, fp16: gu [M, 2I] (gate = columns [0, I), up = [I, 2I)),
+ * q [M, I] int8, scales [M] float32.  I % 8 == 0, I <= 65536.
+ * Replaces vllm_turing/csrc/silu_quant.cu:71 (same arguments).  Returns 0 ok, 1 bad I, 2 launch error. */
+int silu_mul_quant(const void* gu, void* q, void* scales, int M, int I, void* stream);
+
+/* The same for bfloat16 activations.  No counterpart in the reference (its kernel is fp16 only); same codes. */
+int silu_mul_quant_bf16(const void* gu, void* q, void* scales, int M, int I, void* stream);
+
+/* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop (kernel 0: the small-M
+ * streaming kernel, M <= 32; kernel 1: the prefill kernel), for bit-exact accumulator checks.  No counterpart in the
+ * reference.  Returns -1 on bad arguments, else the HIP launch error. */
+int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream);
+
+/* Test export: the device silu of all 65,536 input patterns of dtype, out[65536] uint16 bit patterns.  No
+ * counterpart in the reference.  Returns -1 on bad arguments, else the HIP launch error. */
+int silu_table(void* out, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W8A8_MI355_H */

@@ -19,7 +19,7 @@
  *                       reproduced; rare 1-ulp differences of CUDA's expf are the one unpinned residue).
  *   o_silu_mul_quant    pinned: composition of the above; the fp16 product is exact IEEE.
  *
- * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fno-fast-math; SSE2 float arithmetic on x86-64).
+ * Build: oracle/Makefile (gcc -O3 -ffp-contract=off -fno-fast-math; SSE2 float arithmetic on x86-64).
  */
 #include <math.h>
 #include <stdint.h>

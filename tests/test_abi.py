@@ -1,0 +1,115 @@
+"""CPU-only checks of the C ABI library and the host-side logic (no kernel is launched: no GPU here).
+
+* libw8a8_mi355.so builds for gfx950 and exports every entry point include/w8a8_mi355.h declares;
+* argument validation returns the documented codes before any HIP call;
+* the dispatch predicates (vllm_turing/w8a8.py:38-46,58-66,78-79) select the reference's path for each M and layout;
+* the product package never imports the oracle, and has no torch fallback for the matmul.
+"""
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "w8a8_mi355.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return re.findall(r"^\s*int\s+(\w+)\s*\(", txt, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def L():
+    from vllm_turing_amd import _lib
+    return _lib.lib()
+
+
+def test_header_and_signatures_agree():
+    from vllm_turing_amd import _lib
+    syms = header_symbols()
+    assert sorted(syms) == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_symbol(L):
+    for s in header_symbols():
+        assert hasattr(L, s), s
+
+
+def test_library_is_gfx950_only():
+    from vllm_turing_amd import _build
+    so = _build.so_path()
+    data = open(so, "rb").read()
+    assert b"gfx950" in data
+    assert b"gfx942" not in data and b"gfx90a" not in data
+
+
+def test_argument_validation_codes(L):
+    # w8a8_gemv / w8a8_mma: -1 for M out of range or K % 16 (csrc/w8a8_gemv.cu:349-351, :332-334)
+    assert L.w8a8_gemv(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
+    assert L.w8a8_gemv(16, 16, 0, 0, None, 0, 17, 64, 64, 1, 1, 0, None) == -1
+    assert L.w8a8_gemv(16, 16, 0, 0, None, 0, 4, 64, 40, 1, 1, 0, None) == -1
+    assert L.w8a8_mma(16, 16, 0, 0, None, 0, 33, 64, 64, 1, 1, 0, None) == -1
+    assert L.w8a8_gemv(17, 16, 0, 0, None, 0, 4, 64, 64, 1, 1, 0, None) == -1     # misaligned a
+    assert L.w8a8_gemv(16, 16, 0, 0, None, 0, 4, 64, 64, 1, 1, 2, None) == -1     # bad dtype
+    # w8a8_big: 1 = cannot implement (csrc/w8a8_big.cu:57)
+    assert L.w8a8_big(16, 16, 0, 0, 0, 64, 24, 64, 0, None) == 1                  # N % 16
+    assert L.w8a8_big(16, 16, 0, 0, 0, 64, 64, 72, 0, None) == 1                  # K % 16
+    assert L.w8a8_scaled_mm(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
+    assert L.w8a8_i32(16, 16, 0, 33, 64, 64, 0, None) == -1                       # streaming kernel: M <= 32
+    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 2, None) == -1
+    # silu_mul_quant: 1 = bad I, 0 for M == 0 (csrc/silu_quant.cu:72-73)
+    assert L.silu_mul_quant(None, None, None, 4, 12, None) == 1
+    assert L.silu_mul_quant(None, None, None, 0, 16, None) == 0
+    assert L.silu_mul_quant_bf16(None, None, None, 4, 65544, None) == 1
+    assert L.per_token_quant(None, None, None, 4, 16, 16, 0, None) == -1
+    assert L.per_token_quant(16, 16, 16, 0, 16, 16, 0, None) == 0
+    assert L.silu_table(None, 0, None) == -1
+
+
+def _t(M, N, K, bias=False, per_tensor=False, out_dtype=torch.float16):
+    a = torch.zeros(M, K, dtype=torch.int8)
+    w = torch.zeros(N, K, dtype=torch.int8)
+    sa = torch.ones(1 if per_tensor else M, 1)
+    sb = torch.ones(N, 1)
+    out = torch.empty(M, N, dtype=out_dtype)
+    return out, a, w.t(), sa, sb, (torch.zeros(N, dtype=out_dtype) if bias else None)
+
+
+def path(*args):
+    from vllm_turing_amd import w8a8
+    if w8a8.gemv_ok(*args):
+        return "gemv"
+    if w8a8.mma_ok(*args):
+        return "mma"
+    if w8a8.big_ok(*args):
+        return "big"
+    return "general"
+
+
+@pytest.mark.parametrize("M,kw,want", [
+    (1, {}, "gemv"), (12, {}, "gemv"), (13, {}, "mma"), (32, {}, "mma"), (33, {}, "big"), (4096, {}, "big"),
+    (8, {"bias": True}, "gemv"), (20, {"per_tensor": True}, "mma"), (64, {"bias": True}, "general"),
+    (64, {"per_tensor": True}, "general"), (4, {"out_dtype": torch.float32}, "general"),
+])
+def test_dispatch_truth_table(M, kw, want):
+    assert path(*_t(M, 256, 512, **kw)) == want
+
+
+def test_dispatch_layout_rejections():
+    out, a, b, sa, sb, bias = _t(4, 256, 512)
+    assert path(out, a, b.contiguous(), sa, sb, bias) == "general"        # b not the stride-(1, K) view
+    assert path(out, a[:, :500], b[:500], sa, sb, bias) == "general"      # K % 16
+    out, a, b, sa, sb, bias = _t(40, 250, 512)
+    assert path(out, a, b, sa, sb, bias) == "general"                     # big needs N % 16
+
+
+def test_product_does_not_use_the_oracle():
+    pkg = os.path.join(ROOT, "vllm_turing_amd")
+    for dp, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h")):
+                src = open(os.path.join(dp, f)).read()
+                assert "import oracle" not in src and "from oracle" not in src and "liboracle" not in src, f
+                assert "_int_mm" not in src, f                              # no torch matmul fallback

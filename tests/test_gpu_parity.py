@@ -1,0 +1,333 @@
+"""GPU parity of the HIP W8A8 path against the CPU oracle (bit-exact int8 / int32 / scales; fp16 / bf16 outputs
+bit-exact where the reference's epilogue is pinned, within the fp64 closed form's tolerance otherwise).
+
+Every kernel is called through the C ABI (directly, or through the package's torch custom ops that wrap it).  The
+oracle (oracle/) runs on the CPU on the same seeded inputs.  Full-size configurations are checked on sampled rows
+(the oracle's int32 GEMM restated through torch._int_mm, pinned equal to it in test_oracle_pins.py) and through
+size-independent properties.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import cpu_path
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def L(oracle_lib):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vllm_turing_amd import _lib
+    return _lib.lib()
+
+
+def bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def code(dt):
+    return oracle.FP16 if dt == torch.float16 else oracle.BF16
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# silu: every 16-bit input pattern
+# ---------------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_silu_device_exhaustive(L, dt):
+    say(f"silu_table {dt}")
+    out = torch.empty(65536, dtype=torch.int16, device=DEV)
+    assert L.silu_table(out.data_ptr(), code(dt), stream()) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    ref = oracle.silu_table(code(dt))
+    vals = torch.from_numpy(np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.int16)).view(dt).float()
+    fin = torch.isfinite(vals).numpy()
+    bad = np.nonzero((got != ref) & fin)[0]
+    assert bad.size == 0, f"{bad.size} silu mismatches, first {bad[:8]}"
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# per-token quant
+# ---------------------------------------------------------------------------------------------------------------------
+QUANT_CASES = [(1, 5120), (5, 5120), (16, 5120), (300, 5120), (7, 17408), (3, 136), (4, 8), (2, 131072), (9, 5001), (3, 7),
+               (64, 4104)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K", QUANT_CASES)
+def test_per_token_quant(L, dt, M, K):
+    say(f"per_token_quant M={M} K={K} {dt}")
+    from vllm_turing_amd import per_token_quant
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = (torch.randn(M, K, generator=g) * 3).to(dt)
+    x[0, :] = 0                                            # zero row
+    if M > 2:
+        x[2, K // 3] = 900.0                               # outlier
+    q, s = per_token_quant(x.to(DEV))
+    torch.cuda.synchronize()
+    qr, sr = oracle.quant_rows(x)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(s.cpu().view(-1).numpy(), sr)
+
+
+def test_per_token_quant_strided_rows(L):
+    say("per_token_quant strided")
+    from vllm_turing_amd import per_token_quant
+    g = torch.Generator().manual_seed(3)
+    big = torch.randn(33, 6144, generator=g).half().to(DEV)
+    x = big[:, :5120]                                       # row stride 6144
+    q, s = per_token_quant(x)
+    qr, sr = oracle.quant_rows(x.cpu().contiguous())
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().view(-1).numpy(), sr)
+
+
+def test_per_token_quant_abi_errors(L):
+    assert L.per_token_quant(None, None, None, 4, 16, 16, 0, None) == -1
+    assert L.per_token_quant(1, 1, 1, 4, 16, 8, 0, None) == -1     # ldx < K
+    assert L.per_token_quant(1, 1, 1, 4, 16, 16, 5, None) == -1    # dtype
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# SiLU * up + quant
+# ---------------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,I", [(1, 8704), (7, 8704), (1680, 8704), (300, 4096), (5, 136), (4, 17408), (2, 65536)])
+def test_silu_mul_quant(L, dt, M, I):
+    say(f"silu_mul_quant M={M} I={I} {dt}")
+    from vllm_turing_amd import silu_mul_quant
+    g = torch.Generator().manual_seed(M + I)
+    gu = (torch.randn(M, 2 * I, generator=g) * 3).to(dt)   # tests/test_silu_quant.py:26
+    gu[0, :I] = 0                                          # a zero activation row (tests/test_silu_quant.py:27)
+    q, s = silu_mul_quant(gu.to(DEV))
+    torch.cuda.synchronize()
+    qr, sr, _ = oracle.silu_mul_quant(gu)
+    assert np.array_equal(q.cpu().numpy(), qr), int((q.cpu().numpy() != qr).sum())
+    assert np.array_equal(s.cpu().view(-1).numpy(), sr)
+
+
+def test_silu_mul_quant_codes(L):
+    assert L.silu_mul_quant(None, None, None, 4, 12, None) == 1       # I % 8
+    assert L.silu_mul_quant(None, None, None, 0, 16, None) == 0       # M == 0: nothing to do
+    assert L.silu_mul_quant_bf16(None, None, None, 4, 65544, None) == 1
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# int32 accumulators: bit-exact
+# ---------------------------------------------------------------------------------------------------------------------
+def i32(L, a, w, kernel):
+    M, K = a.shape
+    N = w.shape[0]
+    acc = torch.empty(M, N, dtype=torch.int32, device=DEV)
+    rc = L.w8a8_i32(a.data_ptr(), w.data_ptr(), acc.data_ptr(), M, N, K, kernel, stream())
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return acc.cpu().numpy()
+
+
+STREAM_SHAPES = [(1, 64, 128), (1, 17408, 5120), (2, 1000, 5136), (3, 300, 5168), (4, 256, 16), (8, 17408, 5120),
+                 (13, 7168, 5120), (16, 5120, 8704), (17, 40, 4112), (25, 5120, 3072), (32, 300, 5168),
+                 (31, 8, 48)]
+
+
+@pytest.mark.parametrize("M,N,K", STREAM_SHAPES)
+def test_i32_stream_kernel(L, M, N, K):
+    say(f"i32 stream M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 31 + N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    got = i32(L, a.to(DEV), w.to(DEV), 0)
+    ref = oracle.gemm_i32(a.numpy(), w.numpy())
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+
+
+GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80), (97, 272, 5120),
+               (1024, 768, 1024), (260, 12288, 128)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_i32_gemm_kernel(L, M, N, K):
+    say(f"i32 gemm M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 17 + N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    got = i32(L, a.to(DEV), w.to(DEV), 1)
+    ref = oracle.gemm_i32(a.numpy(), w.numpy())
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+
+
+def test_i32_extreme_values(L):
+    """All -128 (the largest |product|) at K = 17408: 2.85e8 per output, no overflow or saturation difference."""
+    say("i32 extremes")
+    K = 17408
+    a = torch.full((40, K), -128, dtype=torch.int8)
+    w = torch.full((64, K), -128, dtype=torch.int8)
+    w[1::2] = 127
+    for kernel, aa in ((0, a[:8]), (1, a)):
+        got = i32(L, aa.to(DEV), w.to(DEV), kernel)
+        assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), w.numpy()))
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# scaled matmul outputs through the dispatch: bit-exact against the oracle's epilogue for that path
+# ---------------------------------------------------------------------------------------------------------------------
+def run_scaled_mm(a, w, sa, sw, bias, dt):
+    from vllm_turing_amd import cutlass_scaled_mm
+    wd = w.to(DEV)
+    return cutlass_scaled_mm(a.to(DEV), wd.t(), sa.to(DEV), sw.to(DEV), dt, None if bias is None else bias.to(DEV))
+
+
+CASES = [
+    # M, N, K, dtype, bias, per-tensor sa, expected epilogue order
+    (1, 17408, 5120, torch.float16, False, False, 0),      # decode GEMV
+    (4, 7168, 5120, torch.bfloat16, True, False, 0),
+    (8, 5120, 8704, torch.float16, False, True, 0),
+    (12, 1000, 5136, torch.float16, True, False, 0),
+    (13, 5120, 8704, torch.float16, False, False, 0),      # mid band
+    (31, 8192, 5120, torch.bfloat16, True, False, 0),
+    (32, 300, 5168, torch.bfloat16, False, False, 0),
+    (33, 5120, 3072, torch.float16, False, False, 1),      # prefill kernel
+    (300, 1024, 5120, torch.bfloat16, False, False, 1),
+    (512, 12288, 5120, torch.bfloat16, True, False, 1),    # with bias -> general entry, large-M bias chain
+    (100, 1000, 5120, torch.float16, False, True, 1),      # per-tensor sa -> general entry
+]
+
+
+@pytest.mark.parametrize("M,N,K,dt,with_bias,per_tensor,order", CASES)
+def test_scaled_mm_bits(L, M, N, K, dt, with_bias, per_tensor, order):
+    say(f"scaled_mm M={M} N={N} K={K} {dt} bias={with_bias} per_tensor={per_tensor}")
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    sa = torch.rand(1 if per_tensor else M, 1, generator=g) * 1e-2
+    sw = torch.rand(N, 1, generator=g) * 1e-3
+    bias = torch.randn(N, generator=g).to(dt) if with_bias else None
+    out = run_scaled_mm(a, w, sa, sw, bias, dt)
+    torch.cuda.synchronize()
+    acc = cpu_path.scaled_mm(a, w, sa, sw)[1] if M * N * K > 2e9 else torch.from_numpy(
+        oracle.gemm_i32(a.numpy(), w.numpy()))
+    ref = oracle.epilogue(acc.numpy(), sa.numpy(), sw.numpy(), None if bias is None else bits(bias), code(dt), order)
+    got = bits(out)
+    assert np.array_equal(got, ref), f"{int((got != ref).sum())} of {got.size} differ"
+    # and the reference's own fp64 acceptance criterion (tests/test_w8a8_mma.py:43-51)
+    r64 = (a.double() @ w.double().t()) * sa.double() * sw.double().view(1, -1)
+    if bias is not None:
+        r64 = r64 + bias.double()
+    err = ((out.cpu().double() - r64).abs() / (r64.abs() + 1e-3)).max().item()
+    assert err < (4e-3 if dt == torch.float16 else 2e-2)
+
+
+def test_dispatch_paths(L):
+    from vllm_turing_amd import w8a8
+    K, N = 5120, 1024
+    w = torch.zeros(N, K, dtype=torch.int8, device=DEV)
+    sb = torch.ones(N, 1, device=DEV)
+    for M, want in ((1, "gemv"), (12, "gemv"), (13, "mma"), (32, "mma"), (33, "big")):
+        a = torch.zeros(M, K, dtype=torch.int8, device=DEV)
+        sa = torch.ones(M, 1, device=DEV)
+        o = torch.empty(M, N, dtype=torch.float16, device=DEV)
+        got = "gemv" if w8a8.gemv_ok(o, a, w.t(), sa, sb, None) else \
+            "mma" if w8a8.mma_ok(o, a, w.t(), sa, sb, None) else \
+            "big" if w8a8.big_ok(o, a, w.t(), sa, sb, None) else "general"
+        assert got == want, (M, got)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the benchmark configurations at full size
+# ---------------------------------------------------------------------------------------------------------------------
+def test_cpu_case_end_to_end(L):
+    """X fp16 [16, 5120] with 0.5% outlier channels x 20, W int8 [5120, 5120]: quant, GEMV, epilogue all bit-exact."""
+    say("cpu case end to end")
+    from vllm_turing_amd import workloads, per_token_quant, cutlass_scaled_mm
+    c = workloads.cpu_case()
+    x_q, x_s = per_token_quant(c["x"].to(DEV))
+    out = cutlass_scaled_mm(x_q, c["w"].to(DEV).t(), x_s, c["sw"].to(DEV), torch.float16)
+    torch.cuda.synchronize()
+    qr, sr = oracle.quant_rows(c["x"])
+    assert np.array_equal(x_q.cpu().numpy(), qr) and np.array_equal(x_s.cpu().view(-1).numpy(), sr)
+    ref, _ = oracle.scaled_mm(qr, c["w"].numpy(), sr, c["sw"].numpy(), None, oracle.FP16)
+    assert np.array_equal(bits(out), ref)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_decode_config_full(L, M):
+    say(f"decode config M={M}")
+    from vllm_turing_amd import workloads, per_token_quant, cutlass_scaled_mm
+    c = workloads.decode(M)
+    x_q, x_s = per_token_quant(c["x"].to(DEV))
+    out = cutlass_scaled_mm(x_q, c["w"].to(DEV).t(), x_s, c["sw"].to(DEV), torch.float16)
+    torch.cuda.synchronize()
+    qr, sr = oracle.quant_rows(c["x"])
+    ref_out, _ = cpu_path.scaled_mm(torch.from_numpy(qr), c["w"], torch.from_numpy(sr), c["sw"], None, torch.float16, 0)
+    assert torch.equal(out.cpu(), ref_out)
+
+
+@pytest.mark.parametrize("M", [512, 4096])
+def test_prefill_config_sampled(L, M):
+    """C3 at full size: every row of the int32 result is checked on a sample of rows (first, last, random) and the
+    whole result through a linearity property: acc(a1 + a2) == acc(a1) + acc(a2) when no int8 overflows."""
+    say(f"prefill config M={M}")
+    from vllm_turing_amd import workloads, per_token_quant, cutlass_scaled_mm
+    c = workloads.prefill(M)
+    x_q, x_s = per_token_quant(c["x"].to(DEV))
+    wd = c["w"].to(DEV)
+    out = cutlass_scaled_mm(x_q, wd.t(), x_s, c["sw"].to(DEV), torch.bfloat16, c["bias"].to(DEV))
+    acc = torch.empty(M, wd.shape[0], dtype=torch.int32, device=DEV)
+    assert L.w8a8_i32(x_q.data_ptr(), wd.data_ptr(), acc.data_ptr(), M, wd.shape[0], wd.shape[1], 1, stream()) == 0
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.tensor([0, M - 1]), torch.randperm(M, generator=torch.Generator().manual_seed(0))[:30]])
+    qs = x_q.cpu()[rows]
+    acc_ref = torch._int_mm(qs, c["w"].t())
+    assert torch.equal(acc.cpu()[rows], acc_ref)
+    ref = oracle.epilogue(acc_ref.numpy(), x_s.cpu()[rows].numpy(), c["sw"].numpy(), bits(c["bias"]), oracle.BF16, 1)
+    assert np.array_equal(bits(out.cpu()[rows]), ref)
+    # linearity over the whole output: split a into two halves whose sum is a
+    a1 = (x_q // 2).to(torch.int8)
+    a2 = (x_q - a1).to(torch.int8)
+    acc1 = torch.empty_like(acc)
+    acc2 = torch.empty_like(acc)
+    for aa, dst in ((a1, acc1), (a2, acc2)):
+        assert L.w8a8_i32(aa.data_ptr(), wd.data_ptr(), dst.data_ptr(), M, wd.shape[0], wd.shape[1], 1,
+                          stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(acc1 + acc2, acc)
+
+
+def test_mlp_chain_small(L):
+    """gate_up GEMM -> silu_mul_quant -> down GEMM, every intermediate bit-exact (M = 64, the C4 widths)."""
+    say("mlp chain")
+    from vllm_turing_amd import workloads, per_token_quant, mlp_quantized
+    from vllm_turing_amd.tailoverlap import silu_mul_quant
+    from vllm_turing_amd import cutlass_scaled_mm
+    c = workloads.mlp(M=64)
+    x = c["x"]
+    x_q, x_s = per_token_quant(x.to(DEV))
+    wgu, wd = c["w_gate_up"].to(DEV), c["w_down"].to(DEV)
+    gu = cutlass_scaled_mm(x_q, wgu.t(), x_s, c["sw_gate_up"].to(DEV), torch.bfloat16)
+    a_q, a_s = silu_mul_quant(gu)
+    out = cutlass_scaled_mm(a_q, wd.t(), a_s, c["sw_down"].to(DEV), torch.bfloat16)
+    out2 = mlp_quantized(x_q, x_s, wgu, c["sw_gate_up"].to(DEV), wd, c["sw_down"].to(DEV), torch.bfloat16)
+    torch.cuda.synchronize()
+    qr, sr = oracle.quant_rows(x)
+    gu_ref, _ = cpu_path.scaled_mm(torch.from_numpy(qr), c["w_gate_up"], torch.from_numpy(sr), c["sw_gate_up"], None,
+                                   torch.bfloat16, 1)
+    assert torch.equal(gu.cpu(), gu_ref)
+    aq_r, as_r, _ = oracle.silu_mul_quant(gu_ref)
+    assert np.array_equal(a_q.cpu().numpy(), aq_r) and np.array_equal(a_s.cpu().view(-1).numpy(), as_r)
+    o_ref, _ = cpu_path.scaled_mm(torch.from_numpy(aq_r), c["w_down"], torch.from_numpy(as_r), c["sw_down"], None,
+                                  torch.bfloat16, 1)
+    assert torch.equal(out.cpu(), o_ref) and torch.equal(out2.cpu(), o_ref)

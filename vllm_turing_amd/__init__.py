@@ -1,0 +1,35 @@
+"""vllm_turing_amd: the W8A8 SmoothQuant linear path of cookjohn/vllm-turing, rebuilt for AMD Instinct MI355X.
+
+Hand-written gfx950 HIP kernels (per-token int8 quantization, fused SiLU * up + quantization, a weight-streaming
+int8 MFMA GEMV for decode and an LDS-tiled int8 MFMA GEMM for prefill, each with the scale epilogue fused) behind a
+C ABI (include/w8a8_mi355.h) loaded with ctypes, and Python hooks with the reference plugin's signatures:
+  w8a8.cutlass_scaled_mm / torch.ops.vllm_turing_amd.scaled_mm_   (vllm_turing/w8a8.py)
+  quantfuse.scaled_int8_quant / quant_torch                         (vllm_turing/quantfuse.py)
+  tailoverlap.silu_mul_quant                                        (vllm_turing/tailoverlap.py)
+register() mirrors the reference plugin entry point (vllm_turing/__init__.py:38-72): with vLLM importable on a gfx950
+device it patches vllm._custom_ops; VLLM_TURING_DISABLE=1 turns it off.  Importing the package builds nothing; the
+library is built or loaded on first use.
+"""
+import logging
+import os
+
+logger = logging.getLogger("vllm.turing_amd")
+_registered = False
+
+from . import quantfuse, w8a8  # noqa: E402  (defines the custom ops)
+from .linear import W8A8Linear, W8A8LinearMethod  # noqa: E402,F401
+from .quantfuse import per_token_quant, quant_torch, scaled_int8_quant  # noqa: E402,F401
+from .tailoverlap import mlp, mlp_quantized, silu_mul_quant  # noqa: E402,F401
+from .w8a8 import cutlass_scaled_mm  # noqa: E402,F401
+
+
+def register():
+    """Install the hooks into vllm._custom_ops (quantfuse before w8a8, as vllm_turing/__init__.py:61-65)."""
+    global _registered
+    if _registered or os.environ.get("VLLM_TURING_DISABLE", "0") == "1":
+        return
+    _registered = True
+    q = quantfuse.install()
+    m = w8a8.install()
+    logger.info("vllm_turing_amd: scaled_int8_quant hook %s, cutlass_scaled_mm hook %s (GEMV up to M=%d)",
+                "on" if q else "off", "on" if m else "off", w8a8.MAX_M)

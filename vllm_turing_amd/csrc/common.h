@@ -1,0 +1,90 @@
+// Shared device helpers of the W8A8 kernels for gfx950 (CDNA4): fp16/bf16 conversions, the two scale-epilogue
+// chains, int8 quantization and wavefront reductions.  Every file is compiled with -ffp-contract=off: no multiply-add
+// is fused unless written as __builtin_fmaf, so each float operation below is exactly one IEEE rounding.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+enum : int { DT_F16 = 0, DT_BF16 = 1 };
+
+// ---- 16-bit float formats (storage is the raw bit pattern) ---------------------------------------------------------
+struct f16 { uint16_t bits; };
+struct bf16 { uint16_t bits; };
+
+__device__ __forceinline__ float to_float(f16 v) {
+    _Float16 h;
+    __builtin_memcpy(&h, &v.bits, 2);
+    return (float)h;                                   // exact
+}
+__device__ __forceinline__ float to_float(bf16 v) { return __uint_as_float((uint32_t)v.bits << 16); }
+
+template <typename T> __device__ __forceinline__ uint16_t from_float(float x);
+template <> __device__ __forceinline__ uint16_t from_float<f16>(float x) {
+    _Float16 h = (_Float16)x;                          // v_cvt_f16_f32: IEEE round to nearest even
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+template <> __device__ __forceinline__ uint16_t from_float<bf16>(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);   // quiet nan
+    u += 0x7fffu + ((u >> 16) & 1u);                   // round to nearest even; overflow carries to inf
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float lo_half(uint32_t w, f16) { return to_float(f16{(uint16_t)(w & 0xffff)}); }
+__device__ __forceinline__ float hi_half(uint32_t w, f16) { return to_float(f16{(uint16_t)(w >> 16)}); }
+__device__ __forceinline__ float lo_half(uint32_t w, bf16) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_half(uint32_t w, bf16) { return __uint_as_float(w & 0xffff0000u); }
+
+// ---- scale epilogues (int32 accumulator -> float, before the final rounding to T) ----------------------------------
+// Small-M chain of the GEMV / MMA kernels (csrc/w8a8_gemv.cu:91, `(float) acc * sa * sw + b` contracted by nvcc's
+// default --fmad=true):  fma(RN32(float(acc) * sa), sw, b), b = +0 without a bias.
+__device__ __forceinline__ float epi_small(int acc, float sa, float sw, float b) {
+    const float t = (float)acc * sa;
+    return __builtin_fmaf(t, sw, b);
+}
+// Large-M chain (csrc/w8a8_big.cu:26-35: ScaleB, then ScaleA, each rounded to float); with a bias the c2x bias
+// epilogue's multiply-add of ScaleA, the ScaleB product and the bias: fma(sa, RN32(float(acc) * sw), b).
+__device__ __forceinline__ float epi_large(int acc, float sa, float sw) {
+    const float t = (float)acc * sw;
+    return sa * t;
+}
+__device__ __forceinline__ float epi_large_bias(int acc, float sa, float sw, float b) {
+    const float t = (float)acc * sw;
+    return __builtin_fmaf(sa, t, b);
+}
+
+// ---- int8 quantization of one value: round half to even, saturate (csrc/silu_quant.cu:16-20) -----------------------
+__device__ __forceinline__ int q8(float v) {
+    float r = __builtin_rintf(v);                      // v_rndne_f32
+    r = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+    return (int)r;
+}
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)d << 24);
+}
+
+// ---- wavefront (64-lane) reductions ----------------------------------------------------------------------------------
+// DPP row operations combine lanes inside each 16-lane row, ds_swizzle combines the two rows of each 32-lane half,
+// and the two halves meet through readlane.  max and integer add are exact, so the order is free.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = __builtin_fmaxf(v, dpp_f<0xB1>(v));            // quad_perm [1,0,3,2]: lane ^ 1
+    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));            // quad_perm [2,3,0,1]: lane ^ 2
+    v = __builtin_fmaxf(v, dpp_f<0x141>(v));           // row_half_mirror: completes each group of 8
+    v = __builtin_fmaxf(v, dpp_f<0x140>(v));           // row_mirror: completes each row of 16
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));  // lane ^ 16
+    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    return __builtin_fmaxf(lo, hi);                    // wave-uniform
+}
+
+}  // namespace w8

@@ -1,0 +1,390 @@
+// W8A8 int8 x int8 -> int32 matrix products with the fused scale epilogue, for gfx950 (CDNA4).
+//
+//   out[m, n] = RN_T( epilogue( acc[m, n], sa[m], sw[n], bias[n] ) ),  acc[m, n] = sum_k a[m, k] * w[n, k]
+//
+// a: [M, K] int8 row-major (per-token quantized activations); w: [N, K] int8 row-major (the weight as vLLM stores
+// it, passed to cutlass_scaled_mm as its [K, N] stride-(1, K) view); sa: float32 [M] or [1]; sw: float32 [N] or [1];
+// bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
+//
+// Two kernels:
+//  * stream_kernel, M <= 32 (decode and speculative verify): weight-streaming and HBM-bound.  Every wavefront owns
+//    16 weight rows and a slice of K, reads each weight byte exactly once with 16-byte non-temporal loads (a full
+//    128-byte line per row per step) and feeds v_mfma_i32_16x16x64_i8 with the weights as the A operand and up to 16
+//    activation rows per MFMA as the B operand, so the int8 dot products never touch the VALU.  The K slices of a
+//    tile meet in LDS.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
+//  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 4 wavefronts of 128 x 128, each a 4 x 4 grid
+//    of v_mfma_i32_32x32x32_i8; 64-byte K steps double-buffered in LDS with an XOR swizzle of the 16-byte chunks that
+//    keeps ds_read_b128 conflict-free; workgroups remapped so the tiles resident on one XCD share A rows and W rows in
+//    that XCD's L2.  Large-M epilogue chain (csrc/w8a8_big.cu:26-35).
+//
+// Both kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
+// MFMA the same permutation of k on its A and B operands, so every operand load is a contiguous 16-byte vector.
+// Integer accumulation is exact (|acc| < 2^31 for K < 131072), so split-K order and tile order are free and the int32
+// results are bit-exact.
+#include "common.h"
+#include "../../include/w8a8_mi355.h"
+
+namespace w8 {
+
+enum : int { EPI_SMALL = 0, EPI_LARGE = 1, EPI_LARGE_BIAS = 2, EPI_I32 = 3 };
+
+// ---------------------------------------------------------------------------------------------------------------------
+// output write of one element, per epilogue
+// ---------------------------------------------------------------------------------------------------------------------
+template <typename T, int EPI>
+__device__ __forceinline__ void store_out(void* out, long idx, int acc, const float* sa, int m, const float* sw, int n,
+                                          const uint16_t* bias) {
+    if constexpr (EPI == EPI_I32) {
+        static_cast<int*>(out)[idx] = acc;                // no scale is read: sa / sw / bias may be null
+    } else {
+        const float sam = sa[m], swn = sw[n];
+        float r;
+        if constexpr (EPI == EPI_SMALL) r = epi_small(acc, sam, swn, bias ? to_float(T{bias[n]}) : 0.0f);
+        else if constexpr (EPI == EPI_LARGE) r = epi_large(acc, sam, swn);
+        else r = epi_large_bias(acc, sam, swn, to_float(T{bias[n]}));
+        static_cast<uint16_t*>(out)[idx] = from_float<T>(r);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// stream_kernel: M <= 16 * MT rows, weights streamed once
+// ---------------------------------------------------------------------------------------------------------------------
+// Block = 4 wavefronts.  KS wavefronts split the K steps of one 16-row tile (interleaved 128-byte steps, so the
+// wavefronts of a tile read adjacent lines), 4 / KS tiles per block.  U steps of loads are kept in flight per buffer,
+// double-buffered.
+template <typename T, int MT, int KS, int U, int EPI>
+__global__ void __launch_bounds__(256) stream_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                     const float* __restrict__ sa, const float* __restrict__ sw,
+                                                     const uint16_t* __restrict__ bias, void* __restrict__ out,
+                                                     int M, int N, int K, int sa_rows, int sw_rows) {
+    constexpr int TPB = 4 / KS;                          // tiles per block
+    __shared__ int red[KS > 1 ? TPB * (KS - 1) * MT * 4 * 64 : 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ks = wave % KS, tl = wave / KS;
+    const int n0 = (blockIdx.x * TPB + tl) * 16;
+    const int r = lane & 15, g = lane >> 4;
+    const int8_t* wp = w + (long)min(n0 + r, N - 1) * K;
+    const int8_t* ap[MT];
+    bool av[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        av[mt] = mt * 16 + r < M;
+        ap[mt] = a + (long)min(mt * 16 + r, M - 1) * K;
+    }
+    v4i acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+
+    const int nsteps = (K + 127) >> 7;
+    const v4i z = {0, 0, 0, 0};
+    v4i wb[2][U][2], ab[2][U][MT][2];
+    auto load = [&](int buf, int s0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + u * KS;
+            const int k = s * 128 + g * 32;
+            const bool ok0 = s < nsteps && k < K, ok1 = s < nsteps && k + 16 < K;
+            wb[buf][u][0] = ok0 ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + k)) : z;
+            wb[buf][u][1] = ok1 ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + k + 16)) : z;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                ab[buf][u][mt][0] = ok0 && av[mt] ? *reinterpret_cast<const v4i*>(ap[mt] + k) : z;
+                ab[buf][u][mt][1] = ok1 && av[mt] ? *reinterpret_cast<const v4i*>(ap[mt] + k + 16) : z;
+            }
+        }
+    };
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wb[buf][u][0], ab[buf][u][mt][0], acc[mt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wb[buf][u][1], ab[buf][u][mt][1], acc[mt], 0, 0, 0);
+            }
+        }
+    };
+    if (n0 < N) {
+        // ping-pong with compile-time buffer indices (keeps both buffers in registers)
+        int s0 = ks;
+        load(0, s0);
+        while (true) {
+            if (s0 + KS * U < nsteps) load(1, s0 + KS * U);
+            compute(0);
+            s0 += KS * U;
+            if (s0 >= nsteps) break;
+            if (s0 + KS * U < nsteps) load(0, s0 + KS * U);
+            compute(1);
+            s0 += KS * U;
+            if (s0 >= nsteps) break;
+        }
+    }
+    if constexpr (KS > 1) {
+        int* rb = red + (tl * (KS - 1)) * MT * 4 * 64 + lane;
+        if (ks > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) rb[((ks - 1) * MT * 4 + mt * 4 + v) * 64] = acc[mt][v];
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int q = 0; q < KS - 1; ++q)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[mt][v] += rb[(q * MT * 4 + mt * 4 + v) * 64];
+    }
+    if (n0 >= N) return;
+    // D fragment of v_mfma_i32_16x16x64_i8: lane holds rows 4 g + v (weight rows n) of column r (activation row m)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int n = n0 + 4 * g + v;
+            if (n < N) store_out<T, EPI>(out, (long)m * N + n, acc[mt][v], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// gemm_kernel: 256 x 256 tiles, MFMA 32x32x32 int8
+// ---------------------------------------------------------------------------------------------------------------------
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int GROUP_M = 4;                               // tile rows per raster group
+
+// 16-byte chunk c of LDS row `row` lives at chunk position c ^ swz(row): rows that a ds_read_b128 phase serves
+// together (8 consecutive rows with 128-byte LDS phases, 16 with 256-byte phases) land on distinct bank groups.
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+template <typename T, int EPI>
+__global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                   const float* __restrict__ sa, const float* __restrict__ sw,
+                                                   const uint16_t* __restrict__ bias, void* __restrict__ out,
+                                                   int M, int N, int K, int sa_rows, int sw_rows) {
+    __shared__ v4i lds[2][2][BM * (BK / 16)];            // [buffer][A | W][row * 4 + chunk]: 64 KB
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+
+    // XCD-aware remap: hardware places block b on XCD b % 8; give each XCD a contiguous run of tiles
+    const int TM = (M + BM - 1) / BM, TN = (N + BN - 1) / BN;
+    const int nb = gridDim.x, per = nb >> 3;
+    int b = blockIdx.x;
+    if (b < per * 8) b = (b & 7) * per + (b >> 3);
+    const int gsz = GROUP_M * TN, grp = b / gsz, first_m = grp * GROUP_M;
+    const int gm = min(TM - first_m, GROUP_M);
+    const int tm = first_m + (b % gsz) % gm, tn = (b % gsz) / gm;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // global -> LDS: thread loads 4 chunks of A and 4 of W per K step (chunk id = tid + 256 j: row id / 4, chunk id % 4)
+    const int8_t* ga[4];
+    const int8_t* gw[4];
+    int lrow[4], lch[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int id = tid + 256 * j;
+        lrow[j] = id >> 2;
+        lch[j] = id & 3;
+        ga[j] = a + (long)min(m0 + lrow[j], M - 1) * K + lch[j] * 16;
+        gw[j] = w + (long)min(n0 + lrow[j], N - 1) * K + lch[j] * 16;
+    }
+    const v4i z = {0, 0, 0, 0};
+    v4i ra[4], rw[4];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = k0 + lch[j] * 16 < K;
+            ra[j] = ok ? *reinterpret_cast<const v4i*>(ga[j] + k0) : z;
+            rw[j] = ok ? *reinterpret_cast<const v4i*>(gw[j] + k0) : z;
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = lrow[j] * 4 + (lch[j] ^ swz(lrow[j]));
+            lds[buf][0][p] = ra[j];
+            lds[buf][1][p] = rw[j];
+        }
+    };
+
+    const int wm = wave >> 1, wn = wave & 1;
+    v16i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    const int nk = (K + BK - 1) / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int cc = 2 * (lane >> 5) + sub;        // this lane's 16-byte chunk of the 64-byte K step
+            v4i fa[4], fw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = wm * 128 + i * 32 + (lane & 31);
+                fa[i] = lds[buf][0][row * 4 + (cc ^ swz(row))];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = wn * 128 + j * 32 + (lane & 31);
+                fw[j] = lds[buf][1][row * 4 + (cc ^ swz(row))];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fw[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // D fragment of v_mfma_i32_32x32x32_i8: lane holds column lane % 32 (weight row n) and rows
+    // (v & 3) + 4 (lane / 32) + 8 (v / 4) (activation rows m)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 128 + j * 32 + (lane & 31);
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + wm * 128 + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+                if (m < M) store_out<T, EPI>(out, (long)m * N + n, acc[i][j][v], sa, sa_rows ? m : 0, sw,
+                                             sw_rows ? n : 0, bias);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------------------------------------
+struct Args {
+    const int8_t* a;
+    const int8_t* w;
+    const float* sa;
+    const float* sw;
+    const uint16_t* bias;
+    void* out;
+    int M, N, K, sa_rows, sw_rows;
+    hipStream_t st;
+};
+
+template <typename T, int MT, int KS, int U, int EPI>
+static void launch_stream_cfg(const Args& p) {
+    constexpr int TPB = 4 / KS;
+    const int tiles = (p.N + 15) / 16;
+    const int blocks = (tiles + TPB - 1) / TPB;
+    stream_kernel<T, MT, KS, U, EPI><<<blocks, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K,
+                                                               p.sa_rows, p.sw_rows);
+}
+
+template <typename T, int EPI>
+static void launch_stream(const Args& p) {
+    // K split 4 ways per 16-row tile; 4 steps of 128 bytes in flight per buffer
+    if (p.M <= 16) launch_stream_cfg<T, 1, 4, 4, EPI>(p);
+    else launch_stream_cfg<T, 2, 4, 4, EPI>(p);
+}
+
+template <typename T, int EPI>
+static void launch_gemm(const Args& p) {
+    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    gemm_kernel<T, EPI><<<tiles, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows,
+                                                 p.sw_rows);
+}
+
+template <int EPI>
+static void dispatch_dtype_stream(const Args& p, int dtype) {
+    if (dtype == DT_F16) launch_stream<f16, EPI>(p);
+    else launch_stream<bf16, EPI>(p);
+}
+template <int EPI>
+static void dispatch_dtype_gemm(const Args& p, int dtype) {
+    if (dtype == DT_F16) launch_gemm<f16, EPI>(p);
+    else launch_gemm<bf16, EPI>(p);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static int check_common(const void* a, const void* w, int M, int N, int K, int dtype) {
+    if (M < 1 || N < 1 || K < 16 || (K & 15) != 0 || K >= 131072) return -1;
+    if (dtype != DT_F16 && dtype != DT_BF16) return -1;
+    if (!aligned16(a) || !aligned16(w)) return -1;
+    return 0;
+}
+
+}  // namespace w8
+
+using namespace w8;
+
+// The small-M paths.  Same arguments as csrc/w8a8_gemv.cu:347 / :330: a [M, K] int8, w [N, K] int8, sa float32
+// [M] (sa_rows = 1) or [1], sw float32 [N] (sw_rows = 1) or [1], bias [N] of the output type or null, out [M, N];
+// dtype 0 = fp16, 1 = bf16.  Returns -1 on bad arguments, else the HIP error code of the launch (0 = success).
+extern "C" int w8a8_gemv(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out,
+                         int M, int N, int K, int sa_rows, int sw_rows, int dtype, void* stream) {
+    if (M > 16 || check_common(a, w, M, N, K, dtype) != 0) return -1;
+    const Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, out,
+                 M, N, K, sa_rows, sw_rows, (hipStream_t)stream};
+    dispatch_dtype_stream<EPI_SMALL>(p, dtype);
+    return (int)hipGetLastError();
+}
+
+extern "C" int w8a8_mma(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out,
+                        int M, int N, int K, int sa_rows, int sw_rows, int dtype, void* stream) {
+    if (M > 32 || check_common(a, w, M, N, K, dtype) != 0) return -1;
+    const Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, out,
+                 M, N, K, sa_rows, sw_rows, (hipStream_t)stream};
+    dispatch_dtype_stream<EPI_SMALL>(p, dtype);
+    return (int)hipGetLastError();
+}
+
+// The prefill path: csrc/w8a8_big.cu:66 arguments (per-row sa [M], per-column sw [N], no bias).  Return codes as
+// there: 0 ok, 1 cannot implement (shape / alignment), 3 launch failed.
+extern "C" int w8a8_big(const void* A, const void* W, const void* sa, const void* sw, void* out, int M, int N, int K,
+                        int dtype, void* stream) {
+    if (check_common(A, W, M, N, K, dtype) != 0 || (N & 15) != 0) return 1;
+    const Args p{(const int8_t*)A, (const int8_t*)W, (const float*)sa, (const float*)sw, nullptr, out, M, N, K, 1, 1,
+                 (hipStream_t)stream};
+    dispatch_dtype_gemm<EPI_LARGE>(p, dtype);
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// Every shape the reference hands to vLLM's cutlass_scaled_mm fallback (vllm_turing/w8a8.py:117): any M, optional
+// bias, per-row or per-tensor scales, with that op's large-M epilogue (csrc/w8a8_big.cu:26-35; with a bias
+// fma(sa, RN32(acc * sw), b)).  M <= 32 runs the streaming kernel, larger M the prefill kernel.
+// Returns -1 on bad arguments, else the HIP error code of the launch.
+extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, const void* sw, const void* bias,
+                              void* out, int M, int N, int K, int sa_rows, int sw_rows, int dtype, void* stream) {
+    if (check_common(a, w, M, N, K, dtype) != 0) return -1;
+    const Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, out,
+                 M, N, K, sa_rows, sw_rows, (hipStream_t)stream};
+    if (M <= 32) {
+        if (bias) dispatch_dtype_stream<EPI_LARGE_BIAS>(p, dtype);
+        else dispatch_dtype_stream<EPI_LARGE>(p, dtype);
+    } else {
+        if (bias) dispatch_dtype_gemm<EPI_LARGE_BIAS>(p, dtype);
+        else dispatch_dtype_gemm<EPI_LARGE>(p, dtype);
+    }
+    return (int)hipGetLastError();
+}
+
+// Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the small-M streaming
+// kernel, M <= 32; kernel 1 = the prefill kernel).  Returns -1 on bad arguments, else the launch error.
+extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
+    if (check_common(a, w, M, N, K, DT_F16) != 0 || (kernel == 0 && M > 32) || kernel < 0 || kernel > 1) return -1;
+    const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
+                 (hipStream_t)stream};
+    if (kernel == 0) launch_stream<f16, EPI_I32>(p);
+    else launch_gemm<f16, EPI_I32>(p);
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,260 @@
+// Per-token dynamic int8 quantization of W8A8 activations, and the fused SiLU(gate) * up + quantization of the MLP
+// down projection's input, for gfx950.
+//
+// Both are single-pass row reductions: the row is read once from HBM with 16-byte loads into registers, its absmax
+// is reduced inside the wavefront with DPP / ds_swizzle (and across the wavefronts of a block through LDS), and the
+// int8 row is written from the same registers.  HBM traffic is the algorithmic minimum: 2 bytes in and 1 byte out per
+// element (3 in for the SiLU kernel) plus a float32 scale per row.
+//
+// Arithmetic (bit-exact contract):
+//   absmax = max |float(x)|, inverse = absmax > 0 ? 127 / absmax : 0 (IEEE division), scale = absmax / 127,
+//   q = clamp(rint(float(x) * inverse), -128, 127)
+// following vllm_turing/quantfuse.py:18-24 and csrc/silu_quant.cu:57-58,66 (zero-row rule).  The SiLU kernel computes
+// r = RN_T(float(silu(g)) * float(u)) with silu(g) = RN_T(f / (1 + RN32(exp(-f)))) as csrc/silu_quant.cu:11-14,39 does;
+// exp(-f) is evaluated in float64 and rounded once to float32, which equals the correctly rounded float32 exp on every
+// one of the 65,536 fp16 and bf16 inputs (checked exhaustively by the GPU tests against the float32-correct table).
+#include "common.h"
+#include "../../include/w8a8_mi355.h"
+
+namespace w8 {
+
+constexpr int MAX_VPT_QUANT = 16;   // 16-byte vectors per thread kept in registers
+constexpr int MAX_VPT_SILU = 8;
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < nw; ++i) m = __builtin_fmaxf(m, red[i]);
+    return m;
+}
+
+// ---- per-token quant: one block per row, the row in registers ------------------------------------------------------
+template <typename T, int VPT>
+__global__ void __launch_bounds__(1024) per_token_quant_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+                                                               float* __restrict__ scales, int K, long ldx) {
+    __shared__ float red[16];
+    const long row = blockIdx.x;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    const int nvec = K >> 3;
+    uint4 v[VPT];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        v[j] = idx < nvec ? xr[idx] : make_uint4(0, 0, 0, 0);
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(lo_half(w[e], T{})));
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(hi_half(w[e], T{})));
+        }
+    }
+    amax = block_max(amax, red);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (threadIdx.x == 0) scales[row] = amax / 127.0f;
+    uint2* qo = reinterpret_cast<uint2*>(q + row * (long)K);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        if (idx < nvec) {
+            const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            int b[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b[2 * e] = q8(lo_half(w[e], T{}) * inv);
+                b[2 * e + 1] = q8(hi_half(w[e], T{}) * inv);
+            }
+            qo[idx] = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
+        }
+    }
+}
+
+// Any K and alignment: element loop, the row read twice (second read from L2).
+template <typename T>
+__global__ void __launch_bounds__(256) per_token_quant_any_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+                                                                  float* __restrict__ scales, int K, long ldx) {
+    __shared__ float red[16];
+    const long row = blockIdx.x;
+    const uint16_t* xr = x + row * ldx;
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) amax = __builtin_fmaxf(amax, __builtin_fabsf(to_float(T{xr[k]})));
+    amax = block_max(amax, red);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (threadIdx.x == 0) scales[row] = amax / 127.0f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) q[row * (long)K + k] = (int8_t)q8(to_float(T{xr[k]}) * inv);
+}
+
+// ---- SiLU(gate) * up + per-token quant -------------------------------------------------------------------------------
+__device__ __forceinline__ float silu_f(float f) {
+    const float e = (float)exp((double)(-f));              // float64 exp, one rounding to float32
+    const float d = 1.0f + e;
+    return f / d;                                           // IEEE division
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t silu_mul(float g, float u) {
+    const uint16_t sh = from_float<T>(silu_f(g));
+    return from_float<T>(to_float(T{sh}) * u);            // exact float product of two 16-bit values, one rounding
+}
+
+template <typename T, int VPT>
+__global__ void __launch_bounds__(1024) silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
+                                                              float* __restrict__ scales, int I) {
+    __shared__ float red[16];
+    const long row = blockIdx.x;
+    const uint4* g4 = reinterpret_cast<const uint4*>(gu + row * 2 * (long)I);
+    const uint4* u4 = reinterpret_cast<const uint4*>(gu + row * 2 * (long)I + I);
+    const int nvec = I >> 3;
+    uint4 r[VPT];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        uint32_t o[4] = {0, 0, 0, 0};
+        if (idx < nvec) {
+            const uint4 gv = g4[idx], uv = u4[idx];
+            const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+            const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint16_t lo = silu_mul<T>(lo_half(gw[e], T{}), lo_half(uw[e], T{}));
+                const uint16_t hi = silu_mul<T>(hi_half(gw[e], T{}), hi_half(uw[e], T{}));
+                o[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(lo_half(o[e], T{})));
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(hi_half(o[e], T{})));
+            }
+        }
+        r[j] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    amax = block_max(amax, red);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (threadIdx.x == 0) scales[row] = amax / 127.0f;
+    uint2* qo = reinterpret_cast<uint2*>(q + row * (long)I);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        if (idx < nvec) {
+            const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+            int b[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b[2 * e] = q8(lo_half(w[e], T{}) * inv);
+                b[2 * e + 1] = q8(hi_half(w[e], T{}) * inv);
+            }
+            qo[idx] = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
+        }
+    }
+}
+
+// silu of every 16-bit input pattern (test export: the exhaustive check of the device arithmetic).
+template <typename T>
+__global__ void silu_table_kernel(uint16_t* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 65536) out[i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
+}
+
+// ---- launch helpers ------------------------------------------------------------------------------------------------
+// Threads per row: the smallest power-of-two multiple of 64 (<= 1024) that keeps the row within max_vpt vectors.
+static int pick_threads(int nvec, int max_vpt, int* vpt) {
+    int t = 64;
+    while (t < 1024 && (nvec + t - 1) / t > max_vpt) t <<= 1;
+    *vpt = (nvec + t - 1) / t;
+    if (*vpt < 1) *vpt = 1;
+    return t;
+}
+
+template <typename T, int VPT>
+static void launch_ptq(const uint16_t* x, int8_t* q, float* s, int M, int K, long ldx, int threads, hipStream_t st) {
+    per_token_quant_kernel<T, VPT><<<M, threads, 0, st>>>(x, q, s, K, ldx);
+}
+
+template <typename T>
+static int run_ptq(const void* x, void* q, void* s, int M, int K, long ldx, hipStream_t st) {
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    int8_t* qp = static_cast<int8_t*>(q);
+    float* sp = static_cast<float*>(s);
+    const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
+    int vpt = 0;
+    const int threads = pick_threads(K / 8, MAX_VPT_QUANT, &vpt);
+    if (!vec_ok || vpt > MAX_VPT_QUANT) {
+        per_token_quant_any_kernel<T><<<M, 256, 0, st>>>(xp, qp, sp, K, ldx);
+        return 0;
+    }
+    switch (vpt) {
+#define W8_CASE(V) case V: launch_ptq<T, V>(xp, qp, sp, M, K, ldx, threads, st); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8)
+        W8_CASE(9) W8_CASE(10) W8_CASE(11) W8_CASE(12) W8_CASE(13) W8_CASE(14) W8_CASE(15) W8_CASE(16)
+#undef W8_CASE
+        default: return -1;
+    }
+    return 0;
+}
+
+template <typename T>
+static int run_smq(const void* gu, void* q, void* s, int M, int I, hipStream_t st) {
+    int vpt = 0;
+    const int threads = pick_threads(I / 8, MAX_VPT_SILU, &vpt);
+    if (vpt > MAX_VPT_SILU) return 1;
+    const uint16_t* gp = static_cast<const uint16_t*>(gu);
+    int8_t* qp = static_cast<int8_t*>(q);
+    float* sp = static_cast<float*>(s);
+    switch (vpt) {
+#define W8_CASE(V) case V: silu_mul_quant_kernel<T, V><<<M, threads, 0, st>>>(gp, qp, sp, I); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8)
+#undef W8_CASE
+        default: return 1;
+    }
+    return 0;
+}
+
+}  // namespace w8
+
+using namespace w8;
+
+// Dynamic per-token int8 quantization (the eager vllm._custom_ops.scaled_int8_quant the reference leaves to vLLM,
+// vllm_turing/quantfuse.py:35-39).  x: [M, K] fp16 (dtype 0) or bf16 (dtype 1) with row stride ldx elements;
+// q: [M, K] int8 contiguous; scales: [M] float32.  Returns 0, -1 on bad arguments, or the HIP launch error.
+extern "C" int per_token_quant(const void* x, void* q, void* scales, int M, int K, long ldx, int dtype, void* stream) {
+    if (M < 0 || K < 1 || ldx < K || (dtype != DT_F16 && dtype != DT_BF16) || !x || !q || !scales) return -1;
+    if (M == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const int rc = dtype == DT_F16 ? run_ptq<f16>(x, q, scales, M, K, ldx, st) : run_ptq<bf16>(x, q, scales, M, K, ldx, st);
+    if (rc != 0) return rc;
+    return (int)hipGetLastError();
+}
+
+static int smq_entry(const void* gu, void* q, void* scales, int M, int I, int dtype, void* stream) {
+    if (I < 8 || I % 8 != 0 || M < 0) return 1;
+    if ((uintptr_t)gu % 16 != 0 || (uintptr_t)q % 8 != 0) return 1;
+    if (M == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const int rc = dtype == DT_F16 ? run_smq<f16>(gu, q, scales, M, I, st) : run_smq<bf16>(gu, q, scales, M, I, st);
+    if (rc != 0) return rc;
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// SiLU(gate) * up + per-row int8 quantization, fp16 (csrc/silu_quant.cu:71-77: same arguments and return codes:
+// 0 ok, 1 bad I, 2 launch error).  gu: [M, 2I] fp16, q: [M, I] int8, scales: [M] float32.  I % 8 == 0, I <= 65536.
+extern "C" int silu_mul_quant(const void* gu, void* q, void* scales, int M, int I, void* stream) {
+    return smq_entry(gu, q, scales, M, I, DT_F16, stream);
+}
+
+// The same for bf16 activations (no counterpart kernel in the reference, whose kernel is fp16 only; the arithmetic is
+// vLLM's bf16 silu_and_mul followed by the same quantization).
+extern "C" int silu_mul_quant_bf16(const void* gu, void* q, void* scales, int M, int I, void* stream) {
+    return smq_entry(gu, q, scales, M, I, DT_BF16, stream);
+}
+
+// Test export: silu of all 65,536 input patterns of dtype into out[65536] (uint16 bit patterns).
+extern "C" int silu_table(void* out, int dtype, void* stream) {
+    if (!out || (dtype != DT_F16 && dtype != DT_BF16)) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == DT_F16) silu_table_kernel<f16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out));
+    else silu_table_kernel<bf16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out));
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,181 @@
+"""W8A8 scaled int8 matmul behind vLLM's cutlass_scaled_mm, on MI355X (gfx950) HIP kernels.
+
+The counterpart of vllm_turing/w8a8.py.  vLLM's W8A8 int8 linear layers call
+vllm._custom_ops.cutlass_scaled_mm(a, b, scale_a, scale_b, out_dtype, bias); install() replaces that wrapper with one
+that runs the custom op vllm_turing_amd::scaled_mm_ (same arguments as vllm_turing::scaled_mm_, w8a8.py:104-122),
+which dispatches at run time on the concrete M (also under torch.compile and HIP graph capture, where the batch size
+is concrete):
+  * M <= VLLM_TURING_GEMV_MAX_M (default 12)           -> w8a8_gemv   (streaming int8 MFMA kernel, small-M epilogue)
+  * M <= VLLM_TURING_MMA_MAX_M (default and maximum 32) -> w8a8_mma    (same kernel, two 16-row activation tiles)
+  * M > MMA_MAX_M, no bias, per-row / per-column scales -> w8a8_big    (prefill MFMA GEMM, large-M epilogue)
+  * anything else                                       -> w8a8_scaled_mm (prefill or streaming kernel with the
+    large-M epilogue of vLLM's cutlass_scaled_mm, with bias / per-tensor scales; the reference sends these to vLLM's
+    CUTLASS op, w8a8.py:117, or to triton_scaled_mm for non-16-multiple shapes, w8a8.py:141-143)
+The predicates gemv_ok / mma_ok / big_ok keep the reference's layout requirements (w8a8.py:38-46,58-66,78-79).
+Operands that fail them are made conforming (contiguous copies, zero padding of K to a multiple of 16) for the
+general kernel.  Every path runs a HIP kernel; there is no torch fallback.
+"""
+import os
+
+import torch
+
+from . import _lib
+
+MAX_M = int(os.environ.get("VLLM_TURING_GEMV_MAX_M", "12"))
+MMA_MAX_M = min(int(os.environ.get("VLLM_TURING_MMA_MAX_M", "32")), 32)
+BIG = os.environ.get("VLLM_TURING_BIG", "1") != "0"
+GEMV_KERNEL_MAX_M = 16          # what the w8a8_gemv entry point accepts
+
+
+def lib():
+    return _lib.lib()
+
+
+def gemv_ok(out, a, b, sa, sb, bias, max_m=None):
+    """The small-M kernels' layout requirements (vllm_turing/w8a8.py:38-46)."""
+    M, K = a.shape
+    lim = MAX_M if max_m is None else max_m
+    return (1 <= M <= min(lim, GEMV_KERNEL_MAX_M if max_m is None else 32) and K % 16 == 0
+            and a.dtype == torch.int8 and a.is_contiguous()
+            and b.dtype == torch.int8 and b.stride(0) == 1 and b.stride(1) == K
+            and out.is_contiguous() and out.dtype in (torch.float16, torch.bfloat16)
+            and sa.dtype == torch.float32 and sb.dtype == torch.float32
+            and sa.numel() in (1, M) and sb.numel() in (1, b.shape[1])
+            and sa.is_contiguous() and sb.is_contiguous()
+            and (bias is None or (bias.dtype == out.dtype and bias.is_contiguous()))
+            and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+
+
+def mma_ok(out, a, b, sa, sb, bias):
+    """vllm_turing/w8a8.py:78-79."""
+    return a.shape[0] > MAX_M and gemv_ok(out, a, b, sa, sb, bias, MMA_MAX_M)
+
+
+def big_ok(out, a, b, sa, sb, bias):
+    """The prefill kernel's requirements (vllm_turing/w8a8.py:58-66)."""
+    M, K = a.shape
+    N = b.shape[1]
+    return (BIG and M > MMA_MAX_M and bias is None and K % 16 == 0 and N % 16 == 0 and a.dtype == torch.int8
+            and a.is_contiguous() and b.dtype == torch.int8 and b.stride(0) == 1 and b.stride(1) == K
+            and out.is_contiguous() and out.dtype in (torch.float16, torch.bfloat16)
+            and sa.dtype == torch.float32 and sb.dtype == torch.float32 and sa.numel() == M and sb.numel() == N
+            and sa.is_contiguous() and sb.is_contiguous() and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _check(rc, name):
+    if rc != 0:
+        raise RuntimeError(f"{name} failed: {rc}")
+
+
+def gemv(out, a, b, sa, sb, bias):
+    M, K = a.shape
+    N = b.shape[1]
+    _check(lib().w8a8_gemv(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), _ptr(bias), out.data_ptr(),
+                           M, N, K, int(sa.numel() > 1), int(sb.numel() > 1), _lib.dtype_code(out.dtype),
+                           _lib.stream_handle(a.device)), "w8a8_gemv launch")
+
+
+def mma(out, a, b, sa, sb, bias):
+    M, K = a.shape
+    N = b.shape[1]
+    _check(lib().w8a8_mma(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), _ptr(bias), out.data_ptr(),
+                          M, N, K, int(sa.numel() > 1), int(sb.numel() > 1), _lib.dtype_code(out.dtype),
+                          _lib.stream_handle(a.device)), "w8a8_mma launch")
+
+
+def big(out, a, b, sa, sb):
+    M, K = a.shape
+    N = b.shape[1]
+    _check(lib().w8a8_big(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), out.data_ptr(), M, N, K,
+                          _lib.dtype_code(out.dtype), _lib.stream_handle(a.device)), "w8a8_big")
+
+
+def general(out, a, b, sa, sb, bias):
+    """Any layout: conform the operands, then the large-M-epilogue kernel (the CUTLASS-op semantics)."""
+    if out.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"cutlass_scaled_mm output must be float16 or bfloat16, got {out.dtype}")
+    M, K = a.shape
+    N = b.shape[1]
+    a = a.to(torch.int8).contiguous()
+    w = b.t().to(torch.int8).contiguous()                         # [N, K] row-major
+    if K % 16 != 0:                                               # zero columns add nothing to the dot products
+        pad = 16 - K % 16
+        a = torch.nn.functional.pad(a, (0, pad))
+        w = torch.nn.functional.pad(w, (0, pad))
+        K += pad
+    if a.data_ptr() % 16:
+        a = a.clone()
+    if w.data_ptr() % 16:
+        w = w.clone()
+    sa = sa.to(torch.float32).contiguous().reshape(-1)
+    sb = sb.to(torch.float32).contiguous().reshape(-1)
+    if sa.numel() not in (1, M) or sb.numel() not in (1, N):
+        raise ValueError(f"scale shapes {tuple(sa.shape)} / {tuple(sb.shape)} do not match M={M} N={N}")
+    if bias is not None:
+        bias = bias.to(out.dtype).contiguous().reshape(-1)
+    dst = out if out.is_contiguous() else torch.empty((M, N), dtype=out.dtype, device=out.device)
+    _check(lib().w8a8_scaled_mm(a.data_ptr(), w.data_ptr(), sa.data_ptr(), sb.data_ptr(), _ptr(bias), dst.data_ptr(),
+                                M, N, K, int(sa.numel() > 1), int(sb.numel() > 1), _lib.dtype_code(out.dtype),
+                                _lib.stream_handle(a.device)), "w8a8_scaled_mm launch")
+    if dst is not out:
+        out.copy_(dst)
+
+
+_lib_def = torch.library.Library("vllm_turing_amd", "DEF")
+_lib_def.define("scaled_mm_(Tensor(a!) out, Tensor a, Tensor b, Tensor a_scales, Tensor b_scales, Tensor? bias) -> ()")
+
+
+def _scaled_mm_hip(out, a, b, a_scales, b_scales, bias):
+    """Run-time dispatch of vllm_turing/w8a8.py:108-117 onto the HIP kernels."""
+    if a.shape[0] == 0 or b.shape[1] == 0:
+        return
+    if gemv_ok(out, a, b, a_scales, b_scales, bias):
+        gemv(out, a, b, a_scales, b_scales, bias)
+    elif mma_ok(out, a, b, a_scales, b_scales, bias):
+        mma(out, a, b, a_scales, b_scales, bias)
+    elif big_ok(out, a, b, a_scales, b_scales, bias):
+        big(out, a, b, a_scales, b_scales)
+    else:
+        general(out, a, b, a_scales, b_scales, bias)
+
+
+torch.library.impl(_lib_def, "scaled_mm_", "CUDA")(_scaled_mm_hip)
+
+
+@torch.library.register_fake("vllm_turing_amd::scaled_mm_")
+def _scaled_mm_fake(out, a, b, a_scales, b_scales, bias):
+    return None
+
+
+def cutlass_scaled_mm(a, b, scale_a, scale_b, out_dtype, bias=None):
+    """vLLM's cutlass_scaled_mm signature (vllm_turing/w8a8.py:136-147): a int8 [..., K], b int8 [K, N] (the stride-
+    (1, K) view of the [N, K] weight), scale_a float32 [M, 1] or [1], scale_b float32 [N, 1] or [1] -> out [..., N]."""
+    assert out_dtype is torch.bfloat16 or out_dtype is torch.float16
+    assert bias is None or bias.numel() == b.shape[1] and bias.dtype == out_dtype
+    target_shape = (*a.shape[:-1], b.shape[1])
+    a = a.reshape(-1, a.shape[-1])
+    out = torch.empty((a.shape[0], b.shape[1]), dtype=out_dtype, device=a.device)
+    torch.ops.vllm_turing_amd.scaled_mm_(out, a, b, scale_a, scale_b, bias)
+    return out.view(*target_shape)
+
+
+cutlass_scaled_mm._vllm_turing = True
+
+
+def install():
+    """Replace vllm._custom_ops.cutlass_scaled_mm when vLLM is importable and the device is gfx950
+    (vllm_turing/w8a8.py:125-150 gates on sm75)."""
+    try:
+        from vllm import _custom_ops as ops
+    except ImportError:
+        return False
+    if getattr(ops.cutlass_scaled_mm, "_vllm_turing", False):
+        return True
+    if not torch.cuda.is_available() or "gfx950" not in torch.cuda.get_device_properties(0).gcnArchName:
+        return False
+    ops.cutlass_scaled_mm = cutlass_scaled_mm
+    return True
