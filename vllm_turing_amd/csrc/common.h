@@ -25,6 +25,10 @@ __device__ __forceinline__ float to_float(bf16 v) { return __uint_as_float((uint
 
 template <typename T> __device__ __forceinline__ uint16_t from_float(float x);
 template <> __device__ __forceinline__ uint16_t from_float<f16>(float x) {
+    // The barrier keeps x a rounded float32: without it the compiler folds a preceding multiply / fma and this
+    // conversion into one v_fma_mixlo_f16 / v_mad_mixlo_f16, which rounds the exact result once to fp16 instead of
+    // rounding to float32 first, as the reference's __float2half_rn(float) does.
+    asm volatile("" : "+v"(x));
     _Float16 h = (_Float16)x;                          // v_cvt_f16_f32: IEEE round to nearest even
     uint16_t b;
     __builtin_memcpy(&b, &h, 2);
