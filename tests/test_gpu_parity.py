@@ -155,8 +155,23 @@ def test_i32_stream_kernel(L, M, N, K):
     assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
 
 
+DOT4_SHAPES = [(1, 17408, 5120), (2, 17408, 5120), (1, 1000, 5136), (2, 300, 16), (1, 64, 8192), (2, 33, 48),
+               (1, 7, 1040)]
+
+
+@pytest.mark.parametrize("M,N,K", DOT4_SHAPES)
+def test_i32_dot4_kernel(L, M, N, K):
+    say(f"i32 dot4 M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 13 + N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    got = i32(L, a.to(DEV), w.to(DEV), 2)
+    ref = oracle.gemm_i32(a.numpy(), w.numpy())
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+
+
 GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80), (97, 272, 5120),
-               (1024, 768, 1024), (260, 12288, 128)]
+               (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
@@ -177,9 +192,9 @@ def test_i32_extreme_values(L):
     a = torch.full((40, K), -128, dtype=torch.int8)
     w = torch.full((64, K), -128, dtype=torch.int8)
     w[1::2] = 127
-    for kernel, aa in ((0, a[:8]), (1, a)):
-        got = i32(L, aa.to(DEV), w.to(DEV), kernel)
-        assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), w.numpy()))
+    for kernel, aa, ww in ((0, a[:8], w), (1, a, w), (2, a[:2, :8192].contiguous(), w[:, :8192].contiguous())):
+        got = i32(L, aa.to(DEV), ww.to(DEV), kernel)
+        assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), ww.numpy()))
 
 
 # ---------------------------------------------------------------------------------------------------------------------

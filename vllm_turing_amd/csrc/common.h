@@ -91,4 +91,17 @@ __device__ __forceinline__ float wave_max(float v) {
     return __builtin_fmaxf(lo, hi);                    // wave-uniform
 }
 
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+// Sum of an int over the 64 lanes (exact; wave-uniform result).
+__device__ __forceinline__ int wave_sum(int v) {
+    v += dpp_i<0xB1>(v);                               // lane ^ 1
+    v += dpp_i<0x4E>(v);                               // lane ^ 2
+    v += dpp_i<0x141>(v);                              // row_half_mirror: groups of 8
+    v += dpp_i<0x140>(v);                              // row_mirror: rows of 16
+    v += __builtin_amdgcn_ds_swizzle(v, 0x401F);       // lane ^ 16
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
+}
+
 }  // namespace w8

@@ -12,10 +12,14 @@
 //    128-byte line per row per step) and feeds v_mfma_i32_16x16x64_i8 with the weights as the A operand and up to 16
 //    activation rows per MFMA as the B operand, so the int8 dot products never touch the VALU.  The K slices of a
 //    tile meet in LDS.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
+//  * gemv_dot4_kernel, M <= 2 and K <= 8192 (decode): weight-streaming through the VALU: each wavefront instruction
+//    reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in registers, wavefront
+//    reduction with DPP / ds_swizzle.  Small-M epilogue chain.
 //  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 4 wavefronts of 128 x 128, each a 4 x 4 grid
-//    of v_mfma_i32_32x32x32_i8; 64-byte K steps double-buffered in LDS with an XOR swizzle of the 16-byte chunks that
-//    keeps ds_read_b128 conflict-free; workgroups remapped so the tiles resident on one XCD share A rows and W rows in
-//    that XCD's L2.  Large-M epilogue chain (csrc/w8a8_big.cu:26-35).
+//    of v_mfma_i32_32x32x32_i8; 128-byte K stages double-buffered in LDS (128 KB) with an XOR swizzle of the 16-byte
+//    chunks that keeps ds_read_b128 conflict-free, the next stage prefetched into registers during the MFMAs and the
+//    operand fragments of the next 32-byte sub-step read from LDS during the current one; workgroups remapped so the
+//    tiles resident on one XCD share A rows and W rows in that XCD's L2.  Large-M epilogue (csrc/w8a8_big.cu:26-35).
 //
 // Both kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
 // MFMA the same permutation of k on its A and B operands, so every operand load is a contiguous 16-byte vector.
@@ -46,18 +50,25 @@ __device__ __forceinline__ void store_out(void* out, long idx, int acc, const fl
     }
 }
 
+// Weight loads: read once, so non-temporal (global_load_dwordx4 ... nt) by default.
+template <bool NT>
+__device__ __forceinline__ v4i wload(const int8_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+    else return *reinterpret_cast<const v4i*>(p);
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // stream_kernel: M <= 16 * MT rows, weights streamed once
 // ---------------------------------------------------------------------------------------------------------------------
-// Block = 4 wavefronts.  KS wavefronts split the K steps of one 16-row tile (interleaved 128-byte steps, so the
-// wavefronts of a tile read adjacent lines), 4 / KS tiles per block.  U steps of loads are kept in flight per buffer,
-// double-buffered.
-template <typename T, int MT, int KS, int U, int EPI>
-__global__ void __launch_bounds__(256) stream_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+// Block = WPB wavefronts.  KS wavefronts split the K steps of one 16-row tile (interleaved 128-byte steps, so the
+// wavefronts of a tile read adjacent lines), WPB / KS tiles per block.  U steps of loads are kept in flight per
+// buffer, double-buffered.
+template <typename T, int MT, int KS, int U, int WPB, int EPI, bool NT = true>
+__global__ void __launch_bounds__(64 * WPB) stream_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                      const float* __restrict__ sa, const float* __restrict__ sw,
                                                      const uint16_t* __restrict__ bias, void* __restrict__ out,
                                                      int M, int N, int K, int sa_rows, int sw_rows) {
-    constexpr int TPB = 4 / KS;                          // tiles per block
+    constexpr int TPB = WPB / KS;                        // tiles per block
     __shared__ int red[KS > 1 ? TPB * (KS - 1) * MT * 4 * 64 : 1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ks = wave % KS, tl = wave / KS;
@@ -84,8 +95,8 @@ __global__ void __launch_bounds__(256) stream_kernel(const int8_t* __restrict__ 
             const int s = s0 + u * KS;
             const int k = s * 128 + g * 32;
             const bool ok0 = s < nsteps && k < K, ok1 = s < nsteps && k + 16 < K;
-            wb[buf][u][0] = ok0 ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + k)) : z;
-            wb[buf][u][1] = ok1 ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + k + 16)) : z;
+            wb[buf][u][0] = ok0 ? wload<NT>(wp + k) : z;
+            wb[buf][u][1] = ok1 ? wload<NT>(wp + k + 16) : z;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 ab[buf][u][mt][0] = ok0 && av[mt] ? *reinterpret_cast<const v4i*>(ap[mt] + k) : z;
@@ -150,21 +161,104 @@ __global__ void __launch_bounds__(256) stream_kernel(const int8_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// gemv_dot4_kernel: M <= 4 activation rows, weights streamed once through the VALU
+// ---------------------------------------------------------------------------------------------------------------------
+// Every wavefront instruction reads 1 KB of one weight row (64 lanes x 16 contiguous bytes); lane l owns the 16-byte
+// chunks l, l + 64, ... of every row (CH of them), and keeps the matching activation chunks of all M rows in
+// registers for the whole kernel.  Rows are grid-strided over the wavefronts, R rows per iteration with the next
+// iteration's loads issued before this one's v_dot4 math (double buffering).  Each row's per-lane partial sums are
+// reduced across the wavefront with DPP row operations, ds_swizzle and readlane.
+template <typename T, int M, int CH, int R, int EPI, bool NT = false>
+__global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                        const float* __restrict__ sa, const float* __restrict__ sw,
+                                                        const uint16_t* __restrict__ bias, void* __restrict__ out,
+                                                        int N, int K, int sa_rows, int sw_rows) {
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (blockDim.x >> 6);
+    const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int K16 = K >> 4;
+    const v4i z = {0, 0, 0, 0};
+    v4i av[M][CH];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int c = lane + 64 * j;
+            av[m][j] = c < K16 ? *reinterpret_cast<const v4i*>(a + (long)m * K + c * 16) : z;
+        }
+    v4i wb[2][R][CH];
+    auto load = [&](int buf, int n0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = min(n0 + r * nw, N - 1);
+            const int8_t* row = w + (long)n * K;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int c = lane + 64 * j;
+                wb[buf][r][j] = (c < K16 && n0 + r * nw < N) ? wload<NT>(row + c * 16) : z;
+            }
+        }
+    };
+    auto finish = [&](int buf, int n0) {
+        int acc[R][M];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                int s = 0;
+#pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    s = __builtin_amdgcn_sdot4(wb[buf][r][j].x, av[m][j].x, s, false);
+                    s = __builtin_amdgcn_sdot4(wb[buf][r][j].y, av[m][j].y, s, false);
+                    s = __builtin_amdgcn_sdot4(wb[buf][r][j].z, av[m][j].z, s, false);
+                    s = __builtin_amdgcn_sdot4(wb[buf][r][j].w, av[m][j].w, s, false);
+                }
+                acc[r][m] = wave_sum(s);
+            }
+        // lane r * M + m writes output (m, n0 + r * nw)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const int n = n0 + r * nw;
+                if (lane == r * M + m && n < N)
+                    store_out<T, EPI>(out, (long)m * N + n, acc[r][m], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
+            }
+    };
+    const int stride = R * nw;
+    int n0 = wid;
+    if (n0 >= N) return;
+    load(0, n0);
+    while (true) {
+        if (n0 + stride < N) load(1, n0 + stride);
+        finish(0, n0);
+        n0 += stride;
+        if (n0 >= N) break;
+        if (n0 + stride < N) load(0, n0 + stride);
+        finish(1, n0);
+        n0 += stride;
+        if (n0 >= N) break;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
 // gemm_kernel: 256 x 256 tiles, MFMA 32x32x32 int8
 // ---------------------------------------------------------------------------------------------------------------------
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int GROUP_M = 4;                               // tile rows per raster group
+constexpr int GEMM_LDS_BYTES = 2 * 2 * BM * BK;          // [stage][A | W][row][BK bytes] = 128 KB (dynamic LDS)
 
-// 16-byte chunk c of LDS row `row` lives at chunk position c ^ swz(row): rows that a ds_read_b128 phase serves
-// together (8 consecutive rows with 128-byte LDS phases, 16 with 256-byte phases) land on distinct bank groups.
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// 16-byte chunk c of a 128-byte LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
+// (128-byte phases) or 16 rows (256-byte phases) reading the same logical chunk; the XOR puts them on distinct
+// 16-byte bank groups in both cases (rows r and r + 8 that share a position sit in different 128-byte halves).
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 template <typename T, int EPI>
 __global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                    const float* __restrict__ sa, const float* __restrict__ sw,
                                                    const uint16_t* __restrict__ bias, void* __restrict__ out,
                                                    int M, int N, int K, int sa_rows, int sw_rows) {
-    __shared__ v4i lds[2][2][BM * (BK / 16)];            // [buffer][A | W][row * 4 + chunk]: 64 KB
+    extern __shared__ v4i ldsx[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
     // XCD-aware remap: hardware places block b on XCD b % 8; give each XCD a contiguous run of tiles
@@ -178,22 +272,23 @@ __global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a,
     const int m0 = tm * BM, n0 = tn * BN;
 
     // global -> LDS: thread loads 4 chunks of A and 4 of W per K step (chunk id = tid + 256 j: row id / 4, chunk id % 4)
-    const int8_t* ga[4];
-    const int8_t* gw[4];
-    int lrow[4], lch[4];
+    v4i (*lds)[2][BM * 8] = reinterpret_cast<v4i (*)[2][BM * 8]>(ldsx);
+    const int8_t* ga[8];
+    const int8_t* gw[8];
+    int lrow[8], lch[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
         const int id = tid + 256 * j;
-        lrow[j] = id >> 2;
-        lch[j] = id & 3;
+        lrow[j] = id >> 3;
+        lch[j] = id & 7;
         ga[j] = a + (long)min(m0 + lrow[j], M - 1) * K + lch[j] * 16;
         gw[j] = w + (long)min(n0 + lrow[j], N - 1) * K + lch[j] * 16;
     }
     const v4i z = {0, 0, 0, 0};
-    v4i ra[4], rw[4];
+    v4i ra[8], rw[8];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 8; ++j) {
             const bool ok = k0 + lch[j] * 16 < K;
             ra[j] = ok ? *reinterpret_cast<const v4i*>(ga[j] + k0) : z;
             rw[j] = ok ? *reinterpret_cast<const v4i*>(gw[j] + k0) : z;
@@ -201,8 +296,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a,
     };
     auto lstore = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = lrow[j] * 4 + (lch[j] ^ swz(lrow[j]));
+        for (int j = 0; j < 8; ++j) {
+            const int p = lrow[j] * 8 + (lch[j] ^ swz(lrow[j]));
             lds[buf][0][p] = ra[j];
             lds[buf][1][p] = rw[j];
         }
@@ -224,25 +319,29 @@ __global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a,
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
         if (kt + 1 < nk) gload((kt + 1) * BK);
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            const int cc = 2 * (lane >> 5) + sub;        // this lane's 16-byte chunk of the 64-byte K step
-            v4i fa[4], fw[4];
+        v4i fa[2][4], fw[2][4];
+        auto fload = [&](int sub, int fb) {
+            const int cc = 2 * sub + (lane >> 5);        // this lane's 16-byte chunk of the 128-byte K stage
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = wm * 128 + i * 32 + (lane & 31);
-                fa[i] = lds[buf][0][row * 4 + (cc ^ swz(row))];
+                fa[fb][i] = lds[buf][0][row * 8 + (cc ^ swz(row))];
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = wn * 128 + j * 32 + (lane & 31);
-                fw[j] = lds[buf][1][row * 4 + (cc ^ swz(row))];
+                fw[fb][j] = lds[buf][1][row * 8 + (cc ^ swz(row))];
             }
+        };
+        fload(0, 0);
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+            if (sub < 3) fload(sub + 1, (sub + 1) & 1);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fw[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[sub & 1][i], fw[sub & 1][j], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) lstore(buf ^ 1);
         __syncthreads();
@@ -280,27 +379,58 @@ struct Args {
     hipStream_t st;
 };
 
-template <typename T, int MT, int KS, int U, int EPI>
+template <typename T, int MT, int KS, int U, int WPB, int EPI, bool NT = true>
 static void launch_stream_cfg(const Args& p) {
-    constexpr int TPB = 4 / KS;
+    constexpr int TPB = WPB / KS;
     const int tiles = (p.N + 15) / 16;
     const int blocks = (tiles + TPB - 1) / TPB;
-    stream_kernel<T, MT, KS, U, EPI><<<blocks, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K,
+    stream_kernel<T, MT, KS, U, WPB, EPI, NT><<<blocks, 64 * WPB, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K,
                                                                p.sa_rows, p.sw_rows);
 }
 
+// Decode with one or two activation rows: the VALU kernel, one wavefront per two weight rows (measured fastest for
+// K = 5120, N = 17408: every wavefront issues its loads at once and the whole grid is resident).
+constexpr int DOT4_MAX_M = 2, DOT4_MAX_CH = 8;           // K <= 64 * 16 * 8 = 8192
+
+template <typename T, int M, int CH, int EPI>
+static void launch_dot4_ch(const Args& p) {
+    const int waves = (p.N + 1) / 2;
+    gemv_dot4_kernel<T, M, CH, 1, EPI><<<(waves + 3) / 4, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N,
+                                                                            p.K, p.sa_rows, p.sw_rows);
+}
+template <typename T, int M, int EPI>
+static void launch_dot4_m(const Args& p) {
+    switch ((p.K / 16 + 63) / 64) {
+#define W8_CASE(C) case C: launch_dot4_ch<T, M, C, EPI>(p); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8)
+#undef W8_CASE
+    }
+}
+static bool dot4_ok(const Args& p) { return p.M <= DOT4_MAX_M && p.K <= 64 * 16 * DOT4_MAX_CH; }
+
+template <typename T, int EPI>
+static void launch_dot4(const Args& p) {
+    if (p.M == 1) launch_dot4_m<T, 1, EPI>(p);
+    else launch_dot4_m<T, 2, EPI>(p);
+}
+
+// M <= 32: the VALU kernel where it applies, else the MFMA streaming kernel (K split 4 ways per 16-row tile, 4 steps
+// of 128 bytes in flight per buffer; plain loads measured faster than non-temporal ones here).
 template <typename T, int EPI>
 static void launch_stream(const Args& p) {
-    // K split 4 ways per 16-row tile; 4 steps of 128 bytes in flight per buffer
-    if (p.M <= 16) launch_stream_cfg<T, 1, 4, 4, EPI>(p);
-    else launch_stream_cfg<T, 2, 4, 4, EPI>(p);
+    if (dot4_ok(p)) launch_dot4<T, EPI>(p);
+    else if (p.M <= 16) launch_stream_cfg<T, 1, 4, 4, 4, EPI, false>(p);
+    else launch_stream_cfg<T, 2, 4, 4, 4, EPI, false>(p);
 }
 
 template <typename T, int EPI>
 static void launch_gemm(const Args& p) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, EPI>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, GEMM_LDS_BYTES);
+    (void)attr;
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    gemm_kernel<T, EPI><<<tiles, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows,
-                                                 p.sw_rows);
+    gemm_kernel<T, EPI><<<tiles, 256, GEMM_LDS_BYTES, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K,
+                                                               p.sa_rows, p.sw_rows);
 }
 
 template <int EPI>
@@ -378,13 +508,22 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
     return (int)hipGetLastError();
 }
 
-// Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the small-M streaming
-// kernel, M <= 32; kernel 1 = the prefill kernel).  Returns -1 on bad arguments, else the launch error.
+// Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
+// M <= 32; kernel 1 = the prefill kernel; kernel 2 = the VALU dot4 kernel, M <= 2, K <= 8192).  Returns -1 on bad
+// arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
-    if (check_common(a, w, M, N, K, DT_F16) != 0 || (kernel == 0 && M > 32) || kernel < 0 || kernel > 1) return -1;
+    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 2) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
                  (hipStream_t)stream};
-    if (kernel == 0) launch_stream<f16, EPI_I32>(p);
-    else launch_gemm<f16, EPI_I32>(p);
+    if (kernel == 0) {
+        if (M > 32) return -1;
+        if (M <= 16) launch_stream_cfg<f16, 1, 4, 4, 4, EPI_I32, false>(p);
+        else launch_stream_cfg<f16, 2, 4, 4, 4, EPI_I32, false>(p);
+    } else if (kernel == 1) {
+        launch_gemm<f16, EPI_I32>(p);
+    } else {
+        if (!dot4_ok(p)) return -1;
+        launch_dot4<f16, EPI_I32>(p);
+    }
     return (int)hipGetLastError();
 }
