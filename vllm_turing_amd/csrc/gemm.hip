@@ -246,15 +246,164 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
 // ---------------------------------------------------------------------------------------------------------------------
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int GROUP_M = 4;                               // tile rows per raster group
-constexpr int GEMM_LDS_BYTES = 2 * 2 * BM * BK;          // [stage][A | W][row][BK bytes] = 128 KB (dynamic LDS)
+constexpr int EPI_PITCH = 128 * 2 + 8;                  // bytes per row of a wavefront's 128 x 128 output in LDS
+constexpr int GEMM_LDS_BYTES = 4 * 128 * EPI_PITCH;      // >= the two K stages (2 * 2 * BM * BK = 128 KB): 132 KB
+static_assert(GEMM_LDS_BYTES >= 2 * 2 * BM * BK, "LDS holds both K stages");
 
 // 16-byte chunk c of a 128-byte LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
 // (128-byte phases) or 16 rows (256-byte phases) reading the same logical chunk; the XOR puts them on distinct
 // 16-byte bank groups in both cases (rows r and r + 8 that share a position sit in different 128-byte halves).
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
+// Epilogue of one wavefront's 128 x 128 block (4 x 4 MFMA blocks of 32 x 32, weights as the A operand).
 template <typename T, int EPI>
-__global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+__device__ __forceinline__ void store_tile(const v16i (&acc)[4][4], void* out, const float* sa, const float* sw,
+                                           const uint16_t* bias, int M, int N, int sa_rows, int sw_rows, int mb, int nb,
+                                           int lane) {
+    const bool vec = (N & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = mb + i * 32 + (lane & 31);
+        if (m >= M) continue;
+        float sam = 0.0f;
+        if constexpr (EPI != EPI_I32) sam = sa[sa_rows ? m : 0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = nb + j * 32 + 8 * q + 4 * (lane >> 5);
+                if (n >= N) continue;
+                const long idx = (long)m * N + n;
+                if constexpr (EPI == EPI_I32) {
+                    int* o = static_cast<int*>(out);
+                    if (vec && n + 3 < N) {
+                        *reinterpret_cast<v4i*>(o + idx) = v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                               acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    } else {
+                        for (int r = 0; r < 4 && n + r < N; ++r) o[idx + r] = acc[i][j][4 * q + r];
+                    }
+                } else {
+                    uint16_t* o = static_cast<uint16_t*>(out);
+                    if (vec && n + 3 < N) {
+                        float swv[4], bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if (sw_rows) {
+                            const float4 t = *reinterpret_cast<const float4*>(sw + n);
+                            swv[0] = t.x; swv[1] = t.y; swv[2] = t.z; swv[3] = t.w;
+                        } else {
+                            swv[0] = swv[1] = swv[2] = swv[3] = sw[0];
+                        }
+                        if constexpr (EPI == EPI_LARGE_BIAS) {
+                            const uint2 t = *reinterpret_cast<const uint2*>(bias + n);
+                            bv[0] = lo_half(t.x, T{}); bv[1] = hi_half(t.x, T{});
+                            bv[2] = lo_half(t.y, T{}); bv[3] = hi_half(t.y, T{});
+                        }
+                        uint16_t h[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int accv = acc[i][j][4 * q + r];
+                            float v;
+                            if constexpr (EPI == EPI_SMALL) v = epi_small(accv, sam, swv[r], bv[r]);
+                            else if constexpr (EPI == EPI_LARGE) v = epi_large(accv, sam, swv[r]);
+                            else v = epi_large_bias(accv, sam, swv[r], bv[r]);
+                            h[r] = from_float<T>(v);
+                        }
+                        *reinterpret_cast<uint2*>(o + idx) =
+                            make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+                    } else {
+                        for (int r = 0; r < 4 && n + r < N; ++r)
+                            store_out<T, EPI>(out, idx + r, acc[i][j][4 * q + r], sa, sa_rows ? m : 0, sw,
+                                              sw_rows ? n + r : 0, bias);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);           // no hoisting of the next block's loads (register pressure)
+        }
+    }
+}
+
+// Epilogue through LDS: the fragment layout gives each lane 4 consecutive columns of one row, so global stores
+// straight from registers write 8-16 byte pieces of many cache lines (measured at a fraction of HBM write bandwidth).
+// Instead each wavefront writes its 128 x 128 block of finished 16-bit values into its own LDS region (rows padded
+// to 264 bytes: the 8-byte writes of 16 consecutive lanes fall on distinct banks), then reads it back row-major and
+// stores full 128-byte lines (16 lanes x 16 bytes per row).
+template <typename T, int EPI>
+__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], uint8_t* eb, void* out, const float* sa,
+                                               const float* sw, const uint16_t* bias, int M, int N, int sa_rows,
+                                               int sw_rows, int mb, int nb, int lane) {
+    float sam[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sam[i] = sa[sa_rows ? min(mb + i * 32 + (lane & 31), M - 1) : 0];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
+            const int n = nb + nl;
+            float swv[4], bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const bool has_bias = (EPI == EPI_LARGE_BIAS || EPI == EPI_SMALL) && bias != nullptr;
+            if (n + 3 < N && (N & 3) == 0) {                 // four whole columns: vector loads
+                if (sw_rows) {
+                    const float4 t = *reinterpret_cast<const float4*>(sw + n);
+                    swv[0] = t.x; swv[1] = t.y; swv[2] = t.z; swv[3] = t.w;
+                } else {
+                    swv[0] = swv[1] = swv[2] = swv[3] = sw[0];
+                }
+                if (has_bias) {
+                    const uint2 t = *reinterpret_cast<const uint2*>(bias + n);
+                    bv[0] = lo_half(t.x, T{}); bv[1] = hi_half(t.x, T{});
+                    bv[2] = lo_half(t.y, T{}); bv[3] = hi_half(t.y, T{});
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int nn = min(n + r, N - 1);
+                    swv[r] = sw[sw_rows ? nn : 0];
+                    if (has_bias) bv[r] = to_float(T{bias[nn]});
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ml = i * 32 + (lane & 31);
+                uint16_t h[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int accv = acc[i][j][4 * q + r];
+                    float v;
+                    if constexpr (EPI == EPI_SMALL) v = epi_small(accv, sam[i], swv[r], bv[r]);
+                    else if constexpr (EPI == EPI_LARGE) v = epi_large(accv, sam[i], swv[r]);
+                    else v = epi_large_bias(accv, sam[i], swv[r], bv[r]);
+                    h[r] = from_float<T>(v);
+                }
+                *reinterpret_cast<uint2*>(eb + ml * EPI_PITCH + nl * 2) =
+                    make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+            }
+            __builtin_amdgcn_sched_barrier(0);               // no hoisting of the next group's loads
+        }
+    }
+    // the wavefront reads back only what it wrote itself: a wait for its own LDS writes suffices
+    __builtin_amdgcn_s_waitcnt(0xc07f);                  // lgkmcnt(0)
+    const bool vec = (N & 7) == 0;
+    uint16_t* o = static_cast<uint16_t*>(out);
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+        const int rl = it * 4 + (lane >> 4), cl = (lane & 15) * 8;
+        const int m = mb + rl, n = nb + cl;
+        const uint2 lo = *reinterpret_cast<const uint2*>(eb + rl * EPI_PITCH + cl * 2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(eb + rl * EPI_PITCH + cl * 2 + 8);
+        if (m >= M) continue;
+        if (vec && n + 7 < N) {
+            *reinterpret_cast<uint4*>(o + (long)m * N + n) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+            const uint32_t wds[4] = {lo.x, lo.y, hi.x, hi.y};
+            for (int e = 0; e < 8 && n + e < N; ++e)
+                o[(long)m * N + n + e] = (uint16_t)(e & 1 ? wds[e >> 1] >> 16 : wds[e >> 1] & 0xffff);
+        }
+    }
+}
+
+template <typename T, int EPI>
+// One wavefront per SIMD (128 KB of LDS per block, 256 accumulator registers per lane).
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                    const float* __restrict__ sa, const float* __restrict__ sw,
                                                    const uint16_t* __restrict__ bias, void* __restrict__ out,
                                                    int M, int N, int K, int sa_rows, int sw_rows) {
@@ -337,31 +486,29 @@ __global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ a,
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
             if (sub < 3) fload(sub + 1, (sub + 1) & 1);
+            // fences keep the next sub-step's fragment reads ahead of this sub-step's MFMAs (left alone, the
+            // scheduler re-reads each fragment just before its MFMAs and exposes the LDS latency every time)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[sub & 1][i], fw[sub & 1][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub & 1][j], fa[sub & 1][i], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (kt + 1 < nk) lstore(buf ^ 1);
         __syncthreads();
     }
 
-    // D fragment of v_mfma_i32_32x32x32_i8: lane holds column lane % 32 (weight row n) and rows
-    // (v & 3) + 4 (lane / 32) + 8 (v / 4) (activation rows m)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 128 + j * 32 + (lane & 31);
-        if (n >= N) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + wm * 128 + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-                if (m < M) store_out<T, EPI>(out, (long)m * N + n, acc[i][j][v], sa, sa_rows ? m : 0, sw,
-                                             sw_rows ? n : 0, bias);
-            }
-        }
+    // D fragment of v_mfma_i32_32x32x32_i8 with the weights as the A operand: lane holds column lane % 32 of the
+    // 32 x 32 block (activation row m) and its rows 8 q + 4 (lane / 32) + r, q, r = 0..3 (weight rows n): four
+    // consecutive output columns per (q), written as one 8-byte store.
+    if constexpr (EPI == EPI_I32) {
+        store_tile<T, EPI>(acc, out, sa, sw, bias, M, N, sa_rows, sw_rows, m0 + wm * 128, n0 + wn * 128, lane);
+    } else {
+        __syncthreads();                                 // every wavefront is done reading the K stages
+        store_tile_lds<T, EPI>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * 128 * EPI_PITCH, out, sa, sw, bias, M,
+                               N, sa_rows, sw_rows, m0 + wm * 128, n0 + wn * 128, lane);
     }
 }
 
