@@ -25,6 +25,8 @@
 // MFMA the same permutation of k on its A and B operands, so every operand load is a contiguous 16-byte vector.
 // Integer accumulation is exact (|acc| < 2^31 for K < 131072), so split-K order and tile order are free and the int32
 // results are bit-exact.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/w8a8_mi355.h"
 
@@ -244,16 +246,27 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
 // ---------------------------------------------------------------------------------------------------------------------
 // gemm_kernel: 256 x 256 tiles, MFMA 32x32x32 int8
 // ---------------------------------------------------------------------------------------------------------------------
-constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int BM = 256, BN = 256, BK = 64, NSTAGE = 4;
 constexpr int GROUP_M = 4;                               // tile rows per raster group
 constexpr int EPI_PITCH = 128 * 2 + 8;                  // bytes per row of a wavefront's 128 x 128 output in LDS
-constexpr int GEMM_LDS_BYTES = 4 * 128 * EPI_PITCH;      // >= the two K stages (2 * 2 * BM * BK = 128 KB): 132 KB
-static_assert(GEMM_LDS_BYTES >= 2 * 2 * BM * BK, "LDS holds both K stages");
+constexpr int STAGE_BYTES = (BM + BN) * BK;              // one K stage of A and W: 32 KB
+constexpr int GEMM_LDS_BYTES = 4 * 128 * EPI_PITCH;      // the epilogue's 132 KB, which also holds the 4 stages
+static_assert(GEMM_LDS_BYTES >= NSTAGE * STAGE_BYTES, "LDS holds every K stage");
 
-// 16-byte chunk c of a 128-byte LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
-// (128-byte phases) or 16 rows (256-byte phases) reading the same logical chunk; the XOR puts them on distinct
-// 16-byte bank groups in both cases (rows r and r + 8 that share a position sit in different 128-byte halves).
-__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+// 16-byte chunk c of a 64-byte LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
+// (128-byte phases) or 16 rows (256-byte phases) reading the same logical chunk; two 64-byte rows share a 128-byte
+// bank line, so rows of equal parity among 8 (and rows 4 apart among 16) must take distinct positions.  It depends
+// on row & 15 only: the direct-to-LDS loads place a 1 KB block of 16 rows and swizzle by the row within the block.
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ ((row >> 3) & 1)) & 3; }
+
+// s_waitcnt immediate for vmcnt(n) alone (expcnt and lgkmcnt left at their maxima; gfx9 encoding).
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70 | 0xf00; }
+static_assert(NSTAGE == 4, "the waits in gemm_kernel are written for 4 stages of 8 loads per wavefront");
+
+// Raw buffer descriptor over `bytes` bytes (the host checks that M * K and N * K fit 31-bit offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // Epilogue of one wavefront's 128 x 128 block (4 x 4 MFMA blocks of 32 x 32, weights as the A operand).
 template <typename T, int EPI>
@@ -420,35 +433,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int tm = first_m + (b % gsz) % gm, tn = (b % gsz) / gm;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    // global -> LDS: thread loads 4 chunks of A and 4 of W per K step (chunk id = tid + 256 j: row id / 4, chunk id % 4)
-    v4i (*lds)[2][BM * 8] = reinterpret_cast<v4i (*)[2][BM * 8]>(ldsx);
-    const int8_t* ga[8];
-    const int8_t* gw[8];
-    int lrow[8], lch[8];
+    // global -> LDS directly (buffer_load_dwordx4 ... lds): one wavefront instruction fills 1 KB of LDS, i.e. 16
+    // rows of one 64-byte K stage; lane l lands at byte 16 l of it, so it fetches the logical chunk that the swizzle
+    // stores at its position.  Each wavefront issues 4 such loads for A and 4 for W per stage.  NSTAGE stages rotate
+    // in LDS and the loads of stage s + NSTAGE - 1 are issued while stage s is computed, so no register holds staged
+    // data and the memory latency has NSTAGE - 1 stages of MFMA work to hide behind.
+    typedef __attribute__((address_space(3))) void lds_void;
+    const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
+    const int drow = lane >> 2, dch = (lane & 3) ^ swz(drow);   // row within the 16-row block; logical chunk
+    int oa[4], ow[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int id = tid + 256 * j;
-        lrow[j] = id >> 3;
-        lch[j] = id & 7;
-        ga[j] = a + (long)min(m0 + lrow[j], M - 1) * K + lch[j] * 16;
-        gw[j] = w + (long)min(n0 + lrow[j], N - 1) * K + lch[j] * 16;
+    for (int j = 0; j < 4; ++j) {
+        const int row = (wave * 4 + j) * 16 + drow;               // rows 16 (4 wave + j) .. + 16 of the tile
+        oa[j] = min(m0 + row, M - 1) * K + dch * 16;
+        ow[j] = min(n0 + row, N - 1) * K + dch * 16;
     }
-    const v4i z = {0, 0, 0, 0};
-    v4i ra[8], rw[8];
-    auto gload = [&](int k0) {
+    uint8_t* const lbase = reinterpret_cast<uint8_t*>(ldsx);
+    auto issue = [&](int stage, int k0) {
+        uint8_t* sa_l = lbase + stage * STAGE_BYTES;
+        uint8_t* sw_l = sa_l + BM * BK;
+        const bool ok = k0 + dch * 16 < K;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const bool ok = k0 + lch[j] * 16 < K;
-            ra[j] = ok ? *reinterpret_cast<const v4i*>(ga[j] + k0) : z;
-            rw[j] = ok ? *reinterpret_cast<const v4i*>(gw[j] + k0) : z;
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int p = lrow[j] * 8 + (lch[j] ^ swz(lrow[j]));
-            lds[buf][0][p] = ra[j];
-            lds[buf][1][p] = rw[j];
+        for (int j = 0; j < 4; ++j) {
+            const int blk = (wave * 4 + j) * 1024;
+            // past the end of K the offset points outside the buffer: the load returns zeros
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sa_l + blk), 16, ok ? oa[j] : 0x7fffffff, k0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sw_l + blk), 16, ok ? ow[j] : 0x7fffffff, k0, 0, 0);
         }
     };
 
@@ -461,31 +471,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-    const int nk = (K + BK - 1) / BK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
+    auto compute = [&](int stage) {
+        const v4i* la = reinterpret_cast<const v4i*>(lbase + stage * STAGE_BYTES);
+        const v4i* lw = la + BM * (BK / 16);
         v4i fa[2][4], fw[2][4];
         auto fload = [&](int sub, int fb) {
-            const int cc = 2 * sub + (lane >> 5);        // this lane's 16-byte chunk of the 128-byte K stage
+            const int cc = 2 * sub + (lane >> 5);        // this lane's 16-byte chunk of the 64-byte K stage
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = wm * 128 + i * 32 + (lane & 31);
-                fa[fb][i] = lds[buf][0][row * 8 + (cc ^ swz(row))];
+                fa[fb][i] = la[row * 4 + (cc ^ swz(row))];
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = wn * 128 + j * 32 + (lane & 31);
-                fw[fb][j] = lds[buf][1][row * 8 + (cc ^ swz(row))];
+                fw[fb][j] = lw[row * 4 + (cc ^ swz(row))];
             }
         };
         fload(0, 0);
 #pragma unroll
-        for (int sub = 0; sub < 4; ++sub) {
-            if (sub < 3) fload(sub + 1, (sub + 1) & 1);
+        for (int sub = 0; sub < 2; ++sub) {
+            if (sub < 1) fload(sub + 1, (sub + 1) & 1);
             // fences keep the next sub-step's fragment reads ahead of this sub-step's MFMAs (left alone, the
             // scheduler re-reads each fragment just before its MFMAs and exposes the LDS latency every time)
             __builtin_amdgcn_sched_barrier(0);
@@ -493,11 +499,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub & 1][j], fa[sub & 1][i], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub & 1][j], fa[sub & 1][i], acc[i][j], 0, 0,
+                                                                      0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (kt + 1 < nk) lstore(buf ^ 1);
-        __syncthreads();
+    };
+
+    const int nk = (K + BK - 1) / BK;
+#pragma unroll
+    for (int s0 = 0; s0 < NSTAGE - 1; ++s0)
+        if (s0 < nk) issue(s0, s0 * BK);
+    for (int kt = 0; kt < nk; ++kt) {
+        // this wavefront's loads of stage kt are done once at most the later stages' loads (8 per stage) remain
+        const int ahead = min(nk - 1 - kt, NSTAGE - 2);
+        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        // every wavefront's part of stage kt is in LDS (each waited for its own loads above).  A bare s_barrier:
+        // __syncthreads() would also wait for the loads of the later stages still in flight.
+        __builtin_amdgcn_s_barrier();
+        if (kt + NSTAGE - 1 < nk) issue((kt + NSTAGE - 1) % NSTAGE, (kt + NSTAGE - 1) * BK);
+        compute(kt % NSTAGE);
     }
 
     // D fragment of v_mfma_i32_32x32x32_i8 with the weights as the A operand: lane holds column lane % 32 of the
@@ -595,6 +617,7 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 static int check_common(const void* a, const void* w, int M, int N, int K, int dtype) {
     if (M < 1 || N < 1 || K < 16 || (K & 15) != 0 || K >= 131072) return -1;
+    if ((long)M * K >= (1L << 31) || (long)N * K >= (1L << 31)) return -1;    // 32-bit buffer offsets
     if (dtype != DT_F16 && dtype != DT_BF16) return -1;
     if (!aligned16(a) || !aligned16(w)) return -1;
     return 0;
