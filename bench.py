@@ -14,6 +14,9 @@ Also reported:
     bounded sample on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --traffic     (a short fixed launch sequence for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs:
+                                      10 GEMVs over 5 weight copies, a 256 MB device copy for calibrating the counters,
+                                      3 GEMMs, 3 per-token quants, 3 SiLU*up quants; prints nothing else)
 """
 import argparse
 import json
@@ -88,12 +91,58 @@ def cpu_time(fn, budget_s):
     return ts[len(ts) // 2], len(ts)
 
 
+def traffic_sequence(torch, L, st, dev):
+    """Fixed launches for HBM-traffic counters (FETCH_SIZE / WRITE_SIZE per dispatch)."""
+    from vllm_turing_amd import workloads
+    K, N, M = workloads.HIDDEN, workloads.INTERMEDIATE, 1
+    g = torch.Generator(device=dev).manual_seed(1)
+    ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g) for _ in range(5)]
+    xq = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+    xs = torch.rand(M, device=dev, generator=g) * 1e-2
+    sw = torch.rand(N, device=dev, generator=g) * 1e-2
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    for i in range(10):
+        L.w8a8_gemv(xq.data_ptr(), ws[i % 5].data_ptr(), xs.data_ptr(), sw.data_ptr(), None, out.data_ptr(), M, N, K,
+                    1, 1, 0, st())
+    torch.cuda.synchronize()
+    del ws
+    src = torch.ones(256 * 1024 * 1024, dtype=torch.uint8, device=dev)   # calibration: 256 MiB read + write
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    Mg, Ng = 4096, 12288
+    a = torch.randint(-127, 128, (Mg, K), dtype=torch.int8, device=dev, generator=g)
+    w = torch.randint(-127, 128, (Ng, K), dtype=torch.int8, device=dev, generator=g)
+    sa = torch.rand(Mg, device=dev, generator=g) * 1e-2
+    swg = torch.rand(Ng, device=dev, generator=g) * 1e-2
+    bias = torch.randn(Ng, device=dev, generator=g).to(torch.bfloat16)
+    og = torch.empty(Mg, Ng, dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        L.w8a8_scaled_mm(a.data_ptr(), w.data_ptr(), sa.data_ptr(), swg.data_ptr(), bias.data_ptr(), og.data_ptr(), Mg,
+                         Ng, K, 1, 1, 1, st())
+    x = torch.randn(Mg, K, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.empty(Mg, K, dtype=torch.int8, device=dev)
+    s = torch.empty(Mg, device=dev)
+    for _ in range(3):
+        L.per_token_quant(x.data_ptr(), q.data_ptr(), s.data_ptr(), Mg, K, K, 1, st())
+    I = workloads.INTERMEDIATE
+    gu = torch.randn(Mg, 2 * I, device=dev, generator=g).to(torch.bfloat16)
+    qs = torch.empty(Mg, I, dtype=torch.int8, device=dev)
+    ss = torch.empty(Mg, device=dev)
+    for _ in range(3):
+        L.silu_mul_quant_bf16(gu.data_ptr(), qs.data_ptr(), ss.data_ptr(), Mg, I, st())
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
     ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic", action="store_true", help="launch sequence for HBM-traffic counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this W8A8 path has no multi-GPU mode (asked for --gpus {args.gpus})",
@@ -108,7 +157,9 @@ def main():
     torch.cuda.set_device(0)
     L = _lib.lib()
     st = lambda: torch.cuda.current_stream().cuda_stream
-    result = {}
+    if args.traffic:
+        traffic_sequence(torch, L, st, dev)
+        return
 
     # ---- decode GEMV, M=1 -----------------------------------------------------------------------------------------
     M, K, N = 1, workloads.HIDDEN, workloads.INTERMEDIATE
