@@ -1,4 +1,4 @@
-"""The reference's W8A8 linear restated as a vectorised CPU path: TEST / BASELINE INFRASTRUCTURE ONLY.
+"""The reference's W8A8 linear restated as a vectorised CPU path: TEST AND CPU-BASELINE INFRASTRUCTURE ONLY.
 
 This is what bench.py times as the CPU baseline (kind "port") and what the tests use to check full-size shapes
 cheaply: torch's CPU int8 matmul (torch._int_mm, exact int32 results) plus the same float32 epilogue chains as
