@@ -244,110 +244,88 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// gemm_kernel: 256 x 256 tiles, MFMA 32x32x32 int8
+// gemm_kernel: 256 x 256 tiles, MFMA 32x32x32 int8, 64-byte K stages loaded straight into LDS
 // ---------------------------------------------------------------------------------------------------------------------
-constexpr int BM = 256, BN = 256, BK = 64, NSTAGE = 4;
+constexpr int BM = 256, BN = 256;
 constexpr int GROUP_M = 4;                               // tile rows per raster group
-constexpr int EPI_PITCH = 128 * 2 + 8;                  // bytes per row of a wavefront's 128 x 128 output in LDS
-constexpr int STAGE_BYTES = (BM + BN) * BK;              // one K stage of A and W: 32 KB
-constexpr int GEMM_LDS_BYTES = 4 * 128 * EPI_PITCH;      // the epilogue's 132 KB, which also holds the 4 stages
-static_assert(GEMM_LDS_BYTES >= NSTAGE * STAGE_BYTES, "LDS holds every K stage");
 
-// 16-byte chunk c of a 64-byte LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
-// (128-byte phases) or 16 rows (256-byte phases) reading the same logical chunk; two 64-byte rows share a 128-byte
-// bank line, so rows of equal parity among 8 (and rows 4 apart among 16) must take distinct positions.  It depends
-// on row & 15 only: the direct-to-LDS loads place a 1 KB block of 16 rows and swizzle by the row within the block.
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ ((row >> 3) & 1)) & 3; }
+// Wavefront grid 2 x WN over the 256 x 256 tile (each wavefront owns 128 rows of M and 256 / WN columns of N); K is
+// staged KB bytes per row at a time, NS stages rotating in LDS.
+template <int WN, int KB, int NS>
+struct GemmCfg {
+    static constexpr int WAVES = 2 * WN, THREADS = 64 * WAVES;
+    static constexpr int WTN = BN / WN, FN = WTN / 32;   // wavefront tile width, 32-column MFMA blocks in it
+    static constexpr int CPR = KB / 16;                  // 16-byte chunks per staged row
+    static constexpr int RPB = 1024 / KB;                // rows per 1 KB direct-to-LDS block
+    static constexpr int STAGE_BYTES = (BM + BN) * KB;
+    static constexpr int PITCH = WTN * 2 + 8;            // epilogue LDS row: 16-bit outputs + 8 bytes of padding
+    static constexpr int EPI_BYTES = WAVES * 128 * PITCH;
+    static constexpr int LDS_BYTES = EPI_BYTES > NS * STAGE_BYTES ? EPI_BYTES : NS * STAGE_BYTES;
+    static constexpr int BPW = BM / RPB / WAVES;         // 1 KB blocks per wavefront per operand per stage
+    static constexpr int LPW = 2 * BPW;                  // direct-to-LDS loads per wavefront per stage
+    static_assert(NS >= 2 && NS <= 4 && LDS_BYTES <= 160 * 1024, "stage configuration");
+};
+
+// 16-byte chunk c of a staged LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
+// (128-byte phases) or 16 rows (256-byte phases) reading the same logical chunk; the XOR spreads them over distinct
+// 16-byte bank groups in both cases.  With 64-byte rows two rows share a 128-byte bank line (rows of equal parity
+// among 8, and rows 4 apart among 16, must differ); with 128-byte rows every row starts at bank 0 (rows among 8 must
+// differ; rows 8 apart sit in the same 256-byte half only when of equal parity).  Both depend on row & 15 only.
+template <int CPR>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (CPR == 4) return ((row >> 1) ^ ((row >> 3) & 1)) & 3;
+    else return (row ^ ((row >> 3) & 1)) & 7;
+}
 
 // s_waitcnt immediate for vmcnt(n) alone (expcnt and lgkmcnt left at their maxima; gfx9 encoding).
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70 | 0xf00; }
-static_assert(NSTAGE == 4, "the waits in gemm_kernel are written for 4 stages of 8 loads per wavefront");
 
 // Raw buffer descriptor over `bytes` bytes (the host checks that M * K and N * K fit 31-bit offsets).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Epilogue of one wavefront's 128 x 128 block (4 x 4 MFMA blocks of 32 x 32, weights as the A operand).
-template <typename T, int EPI>
-__device__ __forceinline__ void store_tile(const v16i (&acc)[4][4], void* out, const float* sa, const float* sw,
-                                           const uint16_t* bias, int M, int N, int sa_rows, int sw_rows, int mb, int nb,
-                                           int lane) {
+// Raw int32 store of one wavefront's 128 x (32 FN) block (test export only): straight from the fragment layout.
+template <int FN>
+__device__ __forceinline__ void store_tile_i32(const v16i (&acc)[4][FN], int* o, int M, int N, int mb, int nb,
+                                               int lane) {
     const bool vec = (N & 3) == 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = mb + i * 32 + (lane & 31);
         if (m >= M) continue;
-        float sam = 0.0f;
-        if constexpr (EPI != EPI_I32) sam = sa[sa_rows ? m : 0];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FN; ++j) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int n = nb + j * 32 + 8 * q + 4 * (lane >> 5);
                 if (n >= N) continue;
                 const long idx = (long)m * N + n;
-                if constexpr (EPI == EPI_I32) {
-                    int* o = static_cast<int*>(out);
-                    if (vec && n + 3 < N) {
-                        *reinterpret_cast<v4i*>(o + idx) = v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1],
-                                                               acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    } else {
-                        for (int r = 0; r < 4 && n + r < N; ++r) o[idx + r] = acc[i][j][4 * q + r];
-                    }
+                if (vec && n + 3 < N) {
+                    *reinterpret_cast<v4i*>(o + idx) =
+                        v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
                 } else {
-                    uint16_t* o = static_cast<uint16_t*>(out);
-                    if (vec && n + 3 < N) {
-                        float swv[4], bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (sw_rows) {
-                            const float4 t = *reinterpret_cast<const float4*>(sw + n);
-                            swv[0] = t.x; swv[1] = t.y; swv[2] = t.z; swv[3] = t.w;
-                        } else {
-                            swv[0] = swv[1] = swv[2] = swv[3] = sw[0];
-                        }
-                        if constexpr (EPI == EPI_LARGE_BIAS) {
-                            const uint2 t = *reinterpret_cast<const uint2*>(bias + n);
-                            bv[0] = lo_half(t.x, T{}); bv[1] = hi_half(t.x, T{});
-                            bv[2] = lo_half(t.y, T{}); bv[3] = hi_half(t.y, T{});
-                        }
-                        uint16_t h[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int accv = acc[i][j][4 * q + r];
-                            float v;
-                            if constexpr (EPI == EPI_SMALL) v = epi_small(accv, sam, swv[r], bv[r]);
-                            else if constexpr (EPI == EPI_LARGE) v = epi_large(accv, sam, swv[r]);
-                            else v = epi_large_bias(accv, sam, swv[r], bv[r]);
-                            h[r] = from_float<T>(v);
-                        }
-                        *reinterpret_cast<uint2*>(o + idx) =
-                            make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-                    } else {
-                        for (int r = 0; r < 4 && n + r < N; ++r)
-                            store_out<T, EPI>(out, idx + r, acc[i][j][4 * q + r], sa, sa_rows ? m : 0, sw,
-                                              sw_rows ? n + r : 0, bias);
-                    }
+                    for (int r = 0; r < 4 && n + r < N; ++r) o[idx + r] = acc[i][j][4 * q + r];
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);           // no hoisting of the next block's loads (register pressure)
         }
     }
 }
 
 // Epilogue through LDS: the fragment layout gives each lane 4 consecutive columns of one row, so global stores
 // straight from registers write 8-16 byte pieces of many cache lines (measured at a fraction of HBM write bandwidth).
-// Instead each wavefront writes its 128 x 128 block of finished 16-bit values into its own LDS region (rows padded
-// to 264 bytes: the 8-byte writes of 16 consecutive lanes fall on distinct banks), then reads it back row-major and
-// stores full 128-byte lines (16 lanes x 16 bytes per row).
-template <typename T, int EPI>
-__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], uint8_t* eb, void* out, const float* sa,
+// Instead each wavefront writes its 128 x (32 FN) block of finished 16-bit values into its own LDS region (rows
+// padded by 8 bytes: the 8-byte writes of consecutive lanes fall on distinct banks), then reads it back row-major and
+// stores whole 128-byte lines.
+template <typename T, int EPI, int FN, int PITCH>
+__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][FN], uint8_t* eb, void* out, const float* sa,
                                                const float* sw, const uint16_t* bias, int M, int N, int sa_rows,
                                                int sw_rows, int mb, int nb, int lane) {
     float sam[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sam[i] = sa[sa_rows ? min(mb + i * 32 + (lane & 31), M - 1) : 0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < FN; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
@@ -387,22 +365,24 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], uint8_t*
                     else v = epi_large_bias(accv, sam[i], swv[r], bv[r]);
                     h[r] = from_float<T>(v);
                 }
-                *reinterpret_cast<uint2*>(eb + ml * EPI_PITCH + nl * 2) =
+                *reinterpret_cast<uint2*>(eb + ml * PITCH + nl * 2) =
                     make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
             }
             __builtin_amdgcn_sched_barrier(0);               // no hoisting of the next group's loads
         }
     }
     // the wavefront reads back only what it wrote itself: a wait for its own LDS writes suffices
-    __builtin_amdgcn_s_waitcnt(0xc07f);                  // lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0xc07f);                      // lgkmcnt(0)
+    constexpr int LPR = FN * 4;                              // lanes per row: 16 bytes (8 outputs) each
+    constexpr int RPI = 64 / LPR;                            // rows per wavefront instruction
     const bool vec = (N & 7) == 0;
     uint16_t* o = static_cast<uint16_t*>(out);
 #pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
-        const int rl = it * 4 + (lane >> 4), cl = (lane & 15) * 8;
+    for (int it = 0; it < 128 / RPI; ++it) {
+        const int rl = it * RPI + lane / LPR, cl = (lane % LPR) * 8;
         const int m = mb + rl, n = nb + cl;
-        const uint2 lo = *reinterpret_cast<const uint2*>(eb + rl * EPI_PITCH + cl * 2);
-        const uint2 hi = *reinterpret_cast<const uint2*>(eb + rl * EPI_PITCH + cl * 2 + 8);
+        const uint2 lo = *reinterpret_cast<const uint2*>(eb + rl * PITCH + cl * 2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(eb + rl * PITCH + cl * 2 + 8);
         if (m >= M) continue;
         if (vec && n + 7 < N) {
             *reinterpret_cast<uint4*>(o + (long)m * N + n) = make_uint4(lo.x, lo.y, hi.x, hi.y);
@@ -414,12 +394,38 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], uint8_t*
     }
 }
 
-template <typename T, int EPI>
-// One wavefront per SIMD (128 KB of LDS per block, 256 accumulator registers per lane).
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
-                                                   const float* __restrict__ sa, const float* __restrict__ sw,
-                                                   const uint16_t* __restrict__ bias, void* __restrict__ out,
-                                                   int M, int N, int K, int sa_rows, int sw_rows) {
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One K stage of a wavefront's share of A and W (bpw 1 KB blocks of each), straight into LDS.  Block j's lane reads
+// logical chunk ch[j] of its row at offset o*[j]; chunks past the end of K get an offset outside the buffer, which
+// makes the load write zeros.  A plain device function (bpw is a constant after inlining): in a template context the
+// host pass treats the buffer-descriptor type as a substitution failure and silently drops the kernel's host stub.
+__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rsa, __amdgpu_buffer_rsrc_t rsw, uint8_t* stage_l,
+                                          int a_bytes, const int* oa, const int* ow, const int* ch, int bpw, int k0,
+                                          int K, int wave) {
+    uint8_t* sa_l = stage_l;
+    uint8_t* sw_l = stage_l + a_bytes;
+#pragma unroll
+    for (int j = 0; j < bpw; ++j) {
+        const int blk = (wave * bpw + j) * 1024;
+        const bool ok = k0 + ch[j] * 16 < K;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sa_l + blk), 16, ok ? oa[j] : 0x7fffffff, k0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sw_l + blk), 16, ok ? ow[j] : 0x7fffffff, k0, 0, 0);
+    }
+}
+
+// Block of 2 * WN wavefronts (WN = 4: two per SIMD, so one wavefront's LDS and barrier waits are covered by the
+// other's MFMAs).
+template <typename T, int EPI, int WN, int KB, int NS, int GM = GROUP_M, bool PRIO = false>
+__global__ void __launch_bounds__(128 * WN) gemm_kernel(const int8_t* __restrict__ a,
+                                                                    const int8_t* __restrict__ w,
+                                                                    const float* __restrict__ sa,
+                                                                    const float* __restrict__ sw,
+                                                                    const uint16_t* __restrict__ bias,
+                                                                    void* __restrict__ out, int M, int N, int K,
+                                                                    int sa_rows, int sw_rows) {
+    // (GemmCfg<WN, KB, NS>:: spelled out: a local alias of it used inside the lambdas below silently drops the kernel's
+    // host-side stub)
     extern __shared__ v4i ldsx[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
@@ -428,109 +434,106 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int nb = gridDim.x, per = nb >> 3;
     int b = blockIdx.x;
     if (b < per * 8) b = (b & 7) * per + (b >> 3);
-    const int gsz = GROUP_M * TN, grp = b / gsz, first_m = grp * GROUP_M;
-    const int gm = min(TM - first_m, GROUP_M);
+    const int gsz = GM * TN, grp = b / gsz, first_m = grp * GM;
+    const int gm = min(TM - first_m, GM);
     const int tm = first_m + (b % gsz) % gm, tn = (b % gsz) / gm;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    // global -> LDS directly (buffer_load_dwordx4 ... lds): one wavefront instruction fills 1 KB of LDS, i.e. 16
-    // rows of one 64-byte K stage; lane l lands at byte 16 l of it, so it fetches the logical chunk that the swizzle
-    // stores at its position.  Each wavefront issues 4 such loads for A and 4 for W per stage.  NSTAGE stages rotate
-    // in LDS and the loads of stage s + NSTAGE - 1 are issued while stage s is computed, so no register holds staged
-    // data and the memory latency has NSTAGE - 1 stages of MFMA work to hide behind.
-    typedef __attribute__((address_space(3))) void lds_void;
+    // global -> LDS directly (buffer_load_dwordx4 ... lds): one wavefront instruction fills 1 KB of LDS, i.e.
+    // 1024 / KB rows of one stage; lane l lands at byte 16 l of it, so it fetches the logical chunk that the swizzle
+    // stores at its position.  NS stages rotate in LDS and the loads of stage s + NS - 1 are issued while
+    // stage s is computed, so no register holds staged data and the memory latency has NS - 1 stages of MFMA
+    // work to hide behind.
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
-    const int drow = lane >> 2, dch = (lane & 3) ^ swz(drow);   // row within the 16-row block; logical chunk
-    int oa[4], ow[4];
+    using Cfg = GemmCfg<WN, KB, NS>;
+    constexpr int CPR = Cfg::CPR, BPW = Cfg::BPW;
+    const int drow = lane / CPR, pch = lane % CPR;       // row within the 1 KB block; physical chunk position
+    int oa[BPW], ow[BPW], ch[BPW];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = (wave * 4 + j) * 16 + drow;               // rows 16 (4 wave + j) .. + 16 of the tile
-        oa[j] = min(m0 + row, M - 1) * K + dch * 16;
-        ow[j] = min(n0 + row, N - 1) * K + dch * 16;
+    for (int j = 0; j < BPW; ++j) {
+        const int row = (wave * BPW + j) * Cfg::RPB + drow;
+        ch[j] = pch ^ swz<CPR>(row);                     // the logical chunk the swizzle stores at this position
+        oa[j] = min(m0 + row, M - 1) * K + ch[j] * 16;
+        ow[j] = min(n0 + row, N - 1) * K + ch[j] * 16;
     }
     uint8_t* const lbase = reinterpret_cast<uint8_t*>(ldsx);
     auto issue = [&](int stage, int k0) {
-        uint8_t* sa_l = lbase + stage * STAGE_BYTES;
-        uint8_t* sw_l = sa_l + BM * BK;
-        const bool ok = k0 + dch * 16 < K;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int blk = (wave * 4 + j) * 1024;
-            // past the end of K the offset points outside the buffer: the load returns zeros
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sa_l + blk), 16, ok ? oa[j] : 0x7fffffff, k0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sw_l + blk), 16, ok ? ow[j] : 0x7fffffff, k0, 0, 0);
-        }
+        dma_stage(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, ow, ch, BPW, k0, K, wave);
     };
 
-    const int wm = wave >> 1, wn = wave & 1;
-    v16i acc[4][4];
+    const int wm = wave / WN, wn = wave % WN;
+    v16i acc[4][GemmCfg<WN, KB, NS>::FN];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < GemmCfg<WN, KB, NS>::FN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
     auto compute = [&](int stage) {
-        const v4i* la = reinterpret_cast<const v4i*>(lbase + stage * STAGE_BYTES);
-        const v4i* lw = la + BM * (BK / 16);
-        v4i fa[2][4], fw[2][4];
+        const v4i* la = reinterpret_cast<const v4i*>(lbase + stage * Cfg::STAGE_BYTES);
+        const v4i* lw = la + BM * CPR;
+        v4i fa[2][4], fw[2][Cfg::FN];
         auto fload = [&](int sub, int fb) {
-            const int cc = 2 * sub + (lane >> 5);        // this lane's 16-byte chunk of the 64-byte K stage
+            const int cc = 2 * sub + (lane >> 5);        // this lane's 16-byte chunk of the staged row
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = wm * 128 + i * 32 + (lane & 31);
-                fa[fb][i] = la[row * 4 + (cc ^ swz(row))];
+                fa[fb][i] = la[row * CPR + (cc ^ swz<CPR>(row))];
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = wn * 128 + j * 32 + (lane & 31);
-                fw[fb][j] = lw[row * 4 + (cc ^ swz(row))];
+            for (int j = 0; j < Cfg::FN; ++j) {
+                const int row = wn * Cfg::WTN + j * 32 + (lane & 31);
+                fw[fb][j] = lw[row * CPR + (cc ^ swz<CPR>(row))];
             }
         };
+        constexpr int SUBS = KB / 32;                    // MFMA K steps (32 bytes) per stage
         fload(0, 0);
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            if (sub < 1) fload(sub + 1, (sub + 1) & 1);
+        for (int sub = 0; sub < SUBS; ++sub) {
+            if (sub + 1 < SUBS) fload(sub + 1, (sub + 1) & 1);
             // fences keep the next sub-step's fragment reads ahead of this sub-step's MFMAs (left alone, the
             // scheduler re-reads each fragment just before its MFMAs and exposes the LDS latency every time)
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);   // favour the wavefront issuing MFMAs (measured neutral)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < Cfg::FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub & 1][j], fa[sub & 1][i], acc[i][j], 0, 0,
                                                                       0);
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    const int nk = (K + BK - 1) / BK;
+    constexpr int WAIT2 = waitcnt_vm(2 * Cfg::LPW), WAIT1 = waitcnt_vm(Cfg::LPW), WAIT0 = waitcnt_vm(0);
+    const int nk = (K + KB - 1) / KB;
 #pragma unroll
-    for (int s0 = 0; s0 < NSTAGE - 1; ++s0)
-        if (s0 < nk) issue(s0, s0 * BK);
+    for (int s0 = 0; s0 < NS - 1; ++s0)
+        if (s0 < nk) issue(s0, s0 * KB);
     for (int kt = 0; kt < nk; ++kt) {
-        // this wavefront's loads of stage kt are done once at most the later stages' loads (8 per stage) remain
-        const int ahead = min(nk - 1 - kt, NSTAGE - 2);
-        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
-        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
-        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        // this wavefront's loads of stage kt are done once at most the later stages' loads (LPW each) remain
+        const int ahead = min(nk - 1 - kt, NS - 2);
+        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAIT1);
+        else __builtin_amdgcn_s_waitcnt(WAIT0);
         // every wavefront's part of stage kt is in LDS (each waited for its own loads above).  A bare s_barrier:
         // __syncthreads() would also wait for the loads of the later stages still in flight.
         __builtin_amdgcn_s_barrier();
-        if (kt + NSTAGE - 1 < nk) issue((kt + NSTAGE - 1) % NSTAGE, (kt + NSTAGE - 1) * BK);
-        compute(kt % NSTAGE);
+        if (kt + NS - 1 < nk) issue((kt + NS - 1) % NS, (kt + NS - 1) * KB);
+        compute(kt % NS);
     }
 
     // D fragment of v_mfma_i32_32x32x32_i8 with the weights as the A operand: lane holds column lane % 32 of the
-    // 32 x 32 block (activation row m) and its rows 8 q + 4 (lane / 32) + r, q, r = 0..3 (weight rows n): four
-    // consecutive output columns per (q), written as one 8-byte store.
+    // 32 x 32 block (activation row m) and its rows 8 q + 4 (lane / 32) + r, q, r = 0..3 (weight rows n).
+    const int mb = m0 + wm * 128, nbw = n0 + wn * GemmCfg<WN, KB, NS>::WTN;
     if constexpr (EPI == EPI_I32) {
-        store_tile<T, EPI>(acc, out, sa, sw, bias, M, N, sa_rows, sw_rows, m0 + wm * 128, n0 + wn * 128, lane);
+        store_tile_i32<GemmCfg<WN, KB, NS>::FN>(acc, static_cast<int*>(out), M, N, mb, nbw, lane);
     } else {
         __syncthreads();                                 // every wavefront is done reading the K stages
-        store_tile_lds<T, EPI>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * 128 * EPI_PITCH, out, sa, sw, bias, M,
-                               N, sa_rows, sw_rows, m0 + wm * 128, n0 + wn * 128, lane);
+        store_tile_lds<T, EPI, GemmCfg<WN, KB, NS>::FN, GemmCfg<WN, KB, NS>::PITCH>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * 128 * GemmCfg<WN, KB, NS>::PITCH, out,
+                                                sa, sw, bias, M, N, sa_rows, sw_rows, mb, nbw, lane);
     }
 }
 
@@ -592,14 +595,19 @@ static void launch_stream(const Args& p) {
     else launch_stream_cfg<T, 2, 4, 4, 4, EPI, false>(p);
 }
 
-template <typename T, int EPI>
+// 8 wavefronts, 128-byte K stages, 2 in LDS: measured ~9% faster than 64-byte stages x 4 at every prefill shape (half
+// the barriers outweigh the shorter prefetch distance)
+constexpr int GEMM_WN = 4, GEMM_KB = 128, GEMM_NS = 2;
+
+template <typename T, int EPI, int WN = GEMM_WN, int KB = GEMM_KB, int NS = GEMM_NS>
 static void launch_gemm(const Args& p) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, EPI>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, GEMM_LDS_BYTES);
+    using C = GemmCfg<WN, KB, NS>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, EPI, WN, KB, NS>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
     (void)attr;
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    gemm_kernel<T, EPI><<<tiles, 256, GEMM_LDS_BYTES, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K,
-                                                               p.sa_rows, p.sw_rows);
+    gemm_kernel<T, EPI, WN, KB, NS><<<tiles, C::THREADS, C::LDS_BYTES, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
+                                                                               p.M, p.N, p.K, p.sa_rows, p.sw_rows);
 }
 
 template <int EPI>
