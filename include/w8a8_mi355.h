@@ -66,6 +66,11 @@ int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int k
  * counterpart in the reference.  Returns -1 on bad arguments, else the HIP launch error. */
 int silu_table(void* out, int dtype, void* stream);
 
+/* Test export: out[i] (uint16 bit patterns) = the device's round-to-nearest-even of float32 x[i] to fp16 (dtype 0)
+ * or bf16 (dtype 1), the rounding every 16-bit output of this library goes through.  No counterpart in the
+ * reference.  Returns -1 on bad arguments, else the HIP launch error. */
+int f32_to_16(const void* x, void* out, long n, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,9 @@ def test_argument_validation_codes(L):
     assert L.per_token_quant(None, None, None, 4, 16, 16, 0, None) == -1
     assert L.per_token_quant(16, 16, 16, 0, 16, 16, 0, None) == 0
     assert L.silu_table(None, 0, None) == -1
+    assert L.f32_to_16(None, None, 4, 1, None) == -1
+    assert L.f32_to_16(16, 16, 4, 2, None) == -1
+    assert L.f32_to_16(16, 16, 0, 1, None) == 0
 
 
 def _t(M, N, K, bias=False, per_tensor=False, out_dtype=torch.float16):

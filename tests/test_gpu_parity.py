@@ -61,6 +61,38 @@ def test_silu_device_exhaustive(L, dt):
     assert bad.size == 0, f"{bad.size} silu mismatches, first {bad[:8]}"
 
 
+def _rounding_inputs():
+    """Every float32 sign / exponent / top-7-mantissa pattern (the bf16 value grid, 65,536 high halves) combined with
+    the low halves that decide the rounding: 0, 1, just below / at / above the halfway point, the top, and two random
+    ones per high half; the fp16 grid is covered by the same set (its rounding point is bit 12 of the low half)."""
+    hi = np.arange(65536, dtype=np.uint32) << 16
+    lows = [0x0000, 0x0001, 0x7fff, 0x8000, 0x8001, 0xffff, 0x0fff, 0x1000, 0x1001, 0x2000, 0x3000, 0x5000]
+    rng = np.random.default_rng(5)
+    cols = [hi | np.uint32(v) for v in lows] + [hi | rng.integers(0, 65536, 65536, dtype=np.uint32) for _ in range(2)]
+    # fp16's rounding point sits at bit 12 of the float32 mantissa: the same patterns shifted into place
+    cols += [(hi & np.uint32(0xffffe000)) | np.uint32(v) for v in (0x0fff, 0x1000, 0x1001, 0x1fff)]
+    u = np.concatenate(cols)
+    return u.view(np.float32)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_device_rounding(L, dt):
+    say(f"f32_to_16 {dt}")
+    x = _rounding_inputs()
+    xd = torch.from_numpy(x).to(DEV)
+    out = torch.empty(x.size, dtype=torch.int16, device=DEV)
+    assert L.f32_to_16(xd.data_ptr(), out.data_ptr(), x.size, code(dt), stream()) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    ref = torch.from_numpy(x).to(dt).view(torch.int16).numpy().view(np.uint16)
+    fin = np.isfinite(x)
+    bad = np.nonzero((got != ref) & fin)[0]
+    assert bad.size == 0, f"{bad.size} rounding mismatches, first inputs {[hex(int(v)) for v in x.view(np.uint32)[bad[:6]]]}"
+    nan_in = ~fin & (x != np.inf) & (x != -np.inf)
+    g = torch.from_numpy(got[nan_in].view(np.int16)).view(dt).float()
+    assert torch.isnan(g).all()
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # per-token quant
 # ---------------------------------------------------------------------------------------------------------------------

@@ -19,6 +19,7 @@ SIGNATURES = {
     "silu_mul_quant_bf16": [_vp] * 3 + [_i] * 2 + [_vp],
     "w8a8_i32": [_vp] * 3 + [_i] * 4 + [_vp],
     "silu_table": [_vp, _i, _vp],
+    "f32_to_16": [_vp, _vp, _l, _i, _vp],
 }
 
 _lib = None

@@ -159,6 +159,13 @@ __global__ void silu_table_kernel(uint16_t* __restrict__ out) {
     if (i < 65536) out[i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
 }
 
+// float32 -> 16-bit rounding of the epilogues and the SiLU kernel (test export).
+template <typename T>
+__global__ void round16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out, long n) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i < n) out[i] = from_float<T>(x[i]);
+}
+
 // ---- launch helpers ------------------------------------------------------------------------------------------------
 // Threads per row: the smallest power-of-two multiple of 64 (<= 1024) that keeps the row within max_vpt vectors.
 static int pick_threads(int nvec, int max_vpt, int* vpt) {
@@ -257,5 +264,17 @@ extern "C" int silu_table(void* out, int dtype, void* stream) {
     hipStream_t st = (hipStream_t)stream;
     if (dtype == DT_F16) silu_table_kernel<f16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out));
     else silu_table_kernel<bf16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out));
+    return (int)hipGetLastError();
+}
+
+// Test export: out[i] = the device's round-to-nearest-even of x[i] to fp16 (dtype 0) or bf16 (dtype 1), as the
+// epilogues and the SiLU kernel round, for n values.
+extern "C" int f32_to_16(const void* x, void* out, long n, int dtype, void* stream) {
+    if (!x || !out || n < 0 || n > (1L << 40) || (dtype != DT_F16 && dtype != DT_BF16)) return -1;
+    if (n == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const long blocks = (n + 255) / 256;
+    if (dtype == DT_F16) round16_kernel<f16><<<blocks, 256, 0, st>>>(static_cast<const float*>(x), static_cast<uint16_t*>(out), n);
+    else round16_kernel<bf16><<<blocks, 256, 0, st>>>(static_cast<const float*>(x), static_cast<uint16_t*>(out), n);
     return (int)hipGetLastError();
 }
