@@ -11,9 +11,14 @@ Also reported:
   gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline);
   quant: per-token quant at M=4096, K=5120 and SiLU*up+quant at M=4096, I=17408, in GB/s (HBM-bound);
   cpu_baseline: the reference's CPU path restated (oracle/cpu_path.py: torch CPU int8 matmul + dequant), timed on a
-    bounded sample on this host's cores.
+    bounded sample on this host's cores;
+  mlp_chain: the fused MLP chain at M=4096 (per-token quant -> gate_up GEMM N=34816 K=5120 -> SiLU*up+quant
+    I=17408 -> down GEMM N=5120 K=17408, bf16), each kernel's time and roofline fraction and the whole chain;
+  stack: the 64-layer linear stack of the 27B hybrid model (48 GDN + 16 attention mixers, 64 MLPs, 24.3 G int8
+    weights) at M in {1, 4, 4096}: per layer quant -> mixer in-projection -> quant -> mixer out-projection -> quant ->
+    gate_up -> SiLU*up+quant -> down, bf16, one HIP graph per pass; time per pass and per token.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--sections headline,mlp,stack]
        python bench.py --traffic     (a short fixed launch sequence for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs:
                                       10 GEMVs over 5 weight copies, a 256 MB device copy for calibrating the counters,
                                       3 GEMMs, 3 per-token quants, 3 SiLU*up quants; prints nothing else)
@@ -136,6 +141,136 @@ def traffic_sequence(torch, L, st, dev):
     torch.cuda.synchronize()
 
 
+def linear_launch(L, st, a_q, a_s, w, sw, out, M, N, K, dtype_code):
+    """One W8A8 projection through the entry point the reference's dispatch picks for M (no bias): the streaming
+    GEMV for M <= 12, the MMA variant for M <= 32, the prefill GEMM above."""
+    args = (a_q.data_ptr(), w.data_ptr(), a_s.data_ptr(), sw.data_ptr())
+    if M <= 12:
+        rc = L.w8a8_gemv(*args, None, out.data_ptr(), M, N, K, 1, 1, dtype_code, st())
+    elif M <= 32:
+        rc = L.w8a8_mma(*args, None, out.data_ptr(), M, N, K, 1, 1, dtype_code, st())
+    else:
+        rc = L.w8a8_big(*args, out.data_ptr(), M, N, K, dtype_code, st())
+    if rc != 0:
+        raise RuntimeError(f"W8A8 linear M={M} N={N} K={K}: {rc}")
+
+
+def bench_mlp(torch, L, st, dev):
+    """Fused MLP chain at M=4096, bf16: each kernel timed alone (HIP graph of 4 launches) and the chain as a whole."""
+    from vllm_turing_amd import workloads
+    M, H, I = 4096, workloads.HIDDEN, workloads.INTERMEDIATE
+    c = workloads.mlp(M)
+    x = c["x"].to(dev)
+    wgu, swgu = c["w_gate_up"].to(dev), c["sw_gate_up"].to(dev)
+    wd, swd = c["w_down"].to(dev), c["sw_down"].to(dev)
+    x_q = torch.empty(M, H, dtype=torch.int8, device=dev)
+    x_s = torch.empty(M, dtype=torch.float32, device=dev)
+    gu = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=dev)
+    a_q = torch.empty(M, I, dtype=torch.int8, device=dev)
+    a_s = torch.empty(M, dtype=torch.float32, device=dev)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+
+    def quant(i=0):
+        if L.per_token_quant(x.data_ptr(), x_q.data_ptr(), x_s.data_ptr(), M, H, H, 1, st()) != 0:
+            raise RuntimeError("per_token_quant")
+
+    def gate_up(i=0):
+        linear_launch(L, st, x_q, x_s, wgu, swgu, gu, M, 2 * I, H, 1)
+
+    def silu(i=0):
+        if L.silu_mul_quant_bf16(gu.data_ptr(), a_q.data_ptr(), a_s.data_ptr(), M, I, st()) != 0:
+            raise RuntimeError("silu_mul_quant_bf16")
+
+    def down(i=0):
+        linear_launch(L, st, a_q, a_s, wd, swd, out, M, H, I, 1)
+
+    def chain(i=0):
+        quant(); gate_up(); silu(); down()
+
+    res = {"workload": f"MLP chain M={M}: quant [{M},{H}] -> gate_up N={2 * I} K={H} -> SiLU*up+quant I={I} -> "
+                       f"down N={H} K={I}, bf16, SmoothQuant-scaled N(0,1) activations with 0.5% outliers"}
+    t = {}
+    for name, fn, n in (("quant", quant, 10), ("gate_up", gate_up, 4), ("silu_mul_quant", silu, 4), ("down", down, 4),
+                        ("chain", chain, 2)):
+        ms, _ = graph_time(torch, fn, n, 4 * n, n)
+        t[name] = ms
+    ops_gu, ops_d = 2.0 * M * 2 * I * H, 2.0 * M * H * I
+    b_q, b_s = 3 * M * H + 4 * M, 2 * M * 2 * I + M * I + 4 * M
+    res["kernels"] = {
+        "quant": {"us": round(t["quant"] * 1e3, 2), "gbs": round(b_q / t["quant"] / 1e6, 1),
+                  "frac": round(b_q / t["quant"] / 1e6 / HBM_PEAK_GBS, 4)},
+        "gate_up": {"us": round(t["gate_up"] * 1e3, 2), "tops": round(ops_gu / t["gate_up"] / 1e9, 1),
+                    "frac": round(ops_gu / t["gate_up"] / 1e9 / INT8_PEAK_TOPS, 4)},
+        "silu_mul_quant": {"us": round(t["silu_mul_quant"] * 1e3, 2),
+                           "gbs": round(b_s / t["silu_mul_quant"] / 1e6, 1),
+                           "frac": round(b_s / t["silu_mul_quant"] / 1e6 / HBM_PEAK_GBS, 4)},
+        "down": {"us": round(t["down"] * 1e3, 2), "tops": round(ops_d / t["down"] / 1e9, 1),
+                 "frac": round(ops_d / t["down"] / 1e9 / INT8_PEAK_TOPS, 4)},
+    }
+    res["chain_us"] = round(t["chain"] * 1e3, 2)
+    res["chain_tops"] = round((ops_gu + ops_d) / t["chain"] / 1e9, 1)
+    k = res["kernels"]
+    print(f"[bench] MLP chain M={M}: quant {k['quant']['us']} us, gate_up {k['gate_up']['us']} us "
+          f"({k['gate_up']['tops']} TOPS), silu_mul_quant {k['silu_mul_quant']['us']} us, down {k['down']['us']} us "
+          f"({k['down']['tops']} TOPS); chain {res['chain_us']} us", file=sys.stderr, flush=True)
+    return res
+
+
+def bench_stack(torch, L, st, dev, ms_list=(1, 4, 4096)):
+    """64-layer linear stack (random int8 weights and scales per layer), one HIP graph per pass, bf16."""
+    from vllm_turing_amd import workloads
+    shapes = workloads.stack_shapes()
+    g = torch.Generator(device=dev).manual_seed(7)
+    weights = []
+    for (_, _, N, K) in shapes:
+        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        sw = torch.rand(N, device=dev, generator=g) * 9e-3 + 1e-3
+        weights.append((w, sw))
+    n_params = sum(N * K for (_, _, N, K) in shapes)
+    H, I = workloads.HIDDEN, workloads.INTERMEDIATE
+    res = {"workload": f"64-layer linear stack, {len(shapes)} projections, {n_params / 1e9:.2f} G int8 weights, "
+                       f"bf16 activations; per layer quant -> mixer in -> quant -> mixer out -> quant -> gate_up -> "
+                       f"SiLU*up+quant -> down", "passes": {}}
+    for M in ms_list:
+        kmax = max(K for (_, _, _, K) in shapes)
+        nmax = max(N for (_, _, N, _) in shapes)
+        x = torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16)
+        y = torch.randn(M, 6144, device=dev, generator=g).to(torch.bfloat16)
+        q = torch.empty(M * kmax, dtype=torch.int8, device=dev)
+        s = torch.empty(M, dtype=torch.float32, device=dev)
+        o = torch.empty(M * nmax, dtype=torch.bfloat16, device=dev)
+        d = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+
+        def one_pass(i=0):
+            for li, (_, name, N, K) in enumerate(shapes):
+                w, sw = weights[li]
+                if name == "down":
+                    src = o[:M * 2 * I].view(M, 2 * I)          # the gate_up output of this layer
+                    if L.silu_mul_quant_bf16(src.data_ptr(), q.data_ptr(), s.data_ptr(), M, I, st()) != 0:
+                        raise RuntimeError("silu_mul_quant_bf16")
+                    dst = d
+                else:
+                    src = x if K == H else y
+                    if L.per_token_quant(src.data_ptr(), q.data_ptr(), s.data_ptr(), M, K, K, 1, st()) != 0:
+                        raise RuntimeError("per_token_quant")
+                    dst = o
+                linear_launch(L, st, q, s, w, sw, dst, M, N, K, 1)
+
+        ms, _ = graph_time(torch, one_pass, 1, 3, 1)
+        ops = 2.0 * M * n_params
+        entry = {"ms_per_pass": round(ms, 3), "us_per_token": round(ms * 1e3 / M, 3)}
+        if M <= 32:
+            entry["weight_gbs"] = round(n_params / ms / 1e6, 1)
+        else:
+            entry["tops"] = round(ops / ms / 1e9, 1)
+        res["passes"][f"M{M}"] = entry
+        print(f"[bench] stack M={M}: {entry}", file=sys.stderr, flush=True)
+        del x, y, q, s, o, d
+    del weights
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,7 +278,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--traffic", action="store_true", help="launch sequence for HBM-traffic counter runs")
+    ap.add_argument("--sections", default="headline,mlp,stack",
+                    help="comma list: headline (GEMV, GEMM, quant kernels; always run), mlp (MLP chain at M=4096), "
+                         "stack (64-layer sweep)")
     args = ap.parse_args()
+    sections = set(args.sections.split(","))
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this W8A8 path has no multi-GPU mode (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -280,6 +419,13 @@ def main():
                   "silu_mul_quant_M4096_I17408": {"us": round(ms_s * 1e3, 2),
                                                    "gbs": round(smq_bytes / (ms_s * 1e-3) / 1e9, 1)}},
     }
+    if "mlp" in sections:
+        del outg, wg, xq_in, qq, gu, qs
+        torch.cuda.empty_cache()
+        result["mlp_chain"] = bench_mlp(torch, L, st, dev)
+    if "stack" in sections:
+        torch.cuda.empty_cache()
+        result["stack"] = bench_stack(torch, L, st, dev)
     print(json.dumps(result), flush=True)
 
 

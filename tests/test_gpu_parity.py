@@ -173,7 +173,7 @@ def i32(L, a, w, kernel):
 
 STREAM_SHAPES = [(1, 64, 128), (1, 17408, 5120), (2, 1000, 5136), (3, 300, 5168), (4, 256, 16), (8, 17408, 5120),
                  (13, 7168, 5120), (16, 5120, 8704), (17, 40, 4112), (25, 5120, 3072), (32, 300, 5168),
-                 (31, 8, 48)]
+                 (31, 8, 48), (1, 5120, 17408), (4, 5120, 6144), (4, 16384, 5120)]
 
 
 @pytest.mark.parametrize("M,N,K", STREAM_SHAPES)
@@ -203,7 +203,7 @@ def test_i32_dot4_kernel(L, M, N, K):
 
 
 GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80), (97, 272, 5120),
-               (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248)]
+               (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248), (4096, 256, 17408)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
