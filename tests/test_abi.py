@@ -60,7 +60,7 @@ def test_argument_validation_codes(L):
     assert L.w8a8_i32(16, 16, 0, 33, 64, 64, 0, None) == -1                       # streaming kernel: M <= 32
     assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 2, None) == -1                       # VALU kernel: M <= 2
     assert L.w8a8_i32(16, 16, 0, 1, 64, 8208, 2, None) == -1                     # VALU kernel: K <= 8192
-    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 3, None) == -1
+    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 5, None) == -1
     # silu_mul_quant: 1 = bad I, 0 for M == 0 (csrc/silu_quant.cu:72-73)
     assert L.silu_mul_quant(None, None, None, 4, 12, None) == 1
     assert L.silu_mul_quant(None, None, None, 0, 16, None) == 0

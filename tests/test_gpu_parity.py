@@ -206,14 +206,21 @@ GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80
                (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248), (4096, 256, 17408)]
 
 
-@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-def test_i32_gemm_kernel(L, M, N, K):
-    say(f"i32 gemm M={M} N={N} K={K}")
+# prefill kernel as dispatched (1), its small configuration alone (3) and its main configuration alone (4); the
+# 320- and 384-super-tile shapes take the split launch (main for the whole rounds over the CUs, small for the rest)
+GEMM_SPLIT_SHAPES = [(4096, 5120, 256), (2048, 12288, 128), (4160, 5136, 144)]
+
+
+@pytest.mark.parametrize("kernel", [1, 3, 4])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES + GEMM_SPLIT_SHAPES)
+def test_i32_gemm_kernel(L, M, N, K, kernel):
+    say(f"i32 gemm kernel {kernel} M={M} N={N} K={K}")
     g = torch.Generator().manual_seed(M * 17 + N + K)
     a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
     w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
-    got = i32(L, a.to(DEV), w.to(DEV), 1)
-    ref = oracle.gemm_i32(a.numpy(), w.numpy())
+    got = i32(L, a.to(DEV), w.to(DEV), kernel)
+    ref = oracle.gemm_i32(a.numpy(), w.numpy()) if M * N * K < 2e9 else \
+        cpu_path.scaled_mm(a, w, torch.ones(M, 1), torch.ones(N, 1))[1].numpy()
     assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
 
 
@@ -224,7 +231,8 @@ def test_i32_extreme_values(L):
     a = torch.full((40, K), -128, dtype=torch.int8)
     w = torch.full((64, K), -128, dtype=torch.int8)
     w[1::2] = 127
-    for kernel, aa, ww in ((0, a[:8], w), (1, a, w), (2, a[:2, :8192].contiguous(), w[:, :8192].contiguous())):
+    for kernel, aa, ww in ((0, a[:8], w), (1, a, w), (3, a, w), (2, a[:2, :8192].contiguous(),
+                                                                w[:, :8192].contiguous())):
         got = i32(L, aa.to(DEV), ww.to(DEV), kernel)
         assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), ww.numpy()))
 
@@ -251,6 +259,8 @@ CASES = [
     (300, 1024, 5120, torch.bfloat16, False, False, 1),
     (512, 12288, 5120, torch.bfloat16, True, False, 1),    # with bias -> general entry, large-M bias chain
     (100, 1000, 5120, torch.float16, False, True, 1),      # per-tensor sa -> general entry
+    (4096, 5120, 512, torch.bfloat16, True, False, 1),     # 320 super tiles: main + small launches, bias
+    (4160, 5136, 272, torch.float16, False, False, 1),     # ragged edges in both configurations
 ]
 
 

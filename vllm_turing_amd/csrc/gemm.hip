@@ -6,7 +6,7 @@
 // it, passed to cutlass_scaled_mm as its [K, N] stride-(1, K) view); sa: float32 [M] or [1]; sw: float32 [N] or [1];
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
-// Two kernels:
+// Three kernels:
 //  * stream_kernel, M <= 32 (decode and speculative verify): weight-streaming and HBM-bound.  Every wavefront owns
 //    16 weight rows and a slice of K, reads each weight byte exactly once with 16-byte non-temporal loads (a full
 //    128-byte line per row per step) and feeds v_mfma_i32_16x16x64_i8 with the weights as the A operand and up to 16
@@ -15,11 +15,14 @@
 //  * gemv_dot4_kernel, M <= 2 and K <= 8192 (decode): weight-streaming through the VALU: each wavefront instruction
 //    reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in registers, wavefront
 //    reduction with DPP / ds_swizzle.  Small-M epilogue chain.
-//  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 4 wavefronts of 128 x 128, each a 4 x 4 grid
-//    of v_mfma_i32_32x32x32_i8; 128-byte K stages double-buffered in LDS (128 KB) with an XOR swizzle of the 16-byte
-//    chunks that keeps ds_read_b128 conflict-free, the next stage prefetched into registers during the MFMAs and the
-//    operand fragments of the next 32-byte sub-step read from LDS during the current one; workgroups remapped so the
-//    tiles resident on one XCD share A rows and W rows in that XCD's L2.  Large-M epilogue (csrc/w8a8_big.cu:26-35).
+//  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
+//    each a 4 x 2 grid of v_mfma_i32_32x32x32_i8; 128-byte K stages loaded straight from HBM into LDS
+//    (buffer_load ... lds), double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128
+//    conflict-free, and the operand fragments of the next 32-byte sub-step read from LDS during the current one's
+//    MFMAs; workgroups remapped so the tiles resident on one XCD share A rows and W rows in that XCD's L2.  Where the
+//    tiles leave a last partial round over the CUs, that round runs as 128 x 128 quarter tiles (4 wavefronts of
+//    64 x 64, two workgroups per CU) so it spreads over the whole chip.  The epilogue goes through LDS so that every
+//    global store writes whole lines.  Large-M epilogue (csrc/w8a8_big.cu:26-35).
 //
 // Both kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
 // MFMA the same permutation of k on its A and B operands, so every operand load is a contiguous 16-byte vector.
@@ -244,25 +247,34 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// gemm_kernel: 256 x 256 tiles, MFMA 32x32x32 int8, 64-byte K stages loaded straight into LDS
+// gemm_kernel: MFMA 32x32x32 int8 tiles, K stages loaded straight into LDS
 // ---------------------------------------------------------------------------------------------------------------------
-constexpr int BM = 256, BN = 256;
-constexpr int GROUP_M = 4;                               // tile rows per raster group
+// The output is cut into 256 x 256 super tiles, rastered in groups of GROUP_M super-tile rows.  A workgroup computes
+// either a whole super tile (the main configuration) or one 128 x 128 quarter of one (the small configuration, used
+// where the super tiles do not divide evenly over the CUs: the last, partial round of super tiles is done as four
+// times as many quarter tiles, which spreads it over the whole chip).
+constexpr int SUPER = 256;
+constexpr int GROUP_M = 4;                               // super-tile rows per raster group
 
-// Wavefront grid 2 x WN over the 256 x 256 tile (each wavefront owns 128 rows of M and 256 / WN columns of N); K is
-// staged KB bytes per row at a time, NS stages rotating in LDS.
-template <int WN, int KB, int NS>
+// WM x WN wavefronts, each owning FM x FN blocks of 32 x 32 outputs (a (32 FM) x (32 FN) wavefront tile), so the
+// workgroup tile is BM = 32 WM FM rows by BN = 32 WN FN columns.  K is staged KB bytes per row at a time, NS stages
+// rotating in LDS.
+template <int WM, int WN, int FM, int FN, int KB, int NS>
 struct GemmCfg {
-    static constexpr int WAVES = 2 * WN, THREADS = 64 * WAVES;
-    static constexpr int WTN = BN / WN, FN = WTN / 32;   // wavefront tile width, 32-column MFMA blocks in it
+    static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+    static constexpr int WTM = 32 * FM, WTN = 32 * FN;   // wavefront tile
+    static constexpr int BM = WM * WTM, BN = WN * WTN;   // workgroup tile
+    static constexpr int SUB = (SUPER / BM) * (SUPER / BN);   // workgroup tiles per super tile
     static constexpr int CPR = KB / 16;                  // 16-byte chunks per staged row
     static constexpr int RPB = 1024 / KB;                // rows per 1 KB direct-to-LDS block
     static constexpr int STAGE_BYTES = (BM + BN) * KB;
     static constexpr int PITCH = WTN * 2 + 8;            // epilogue LDS row: 16-bit outputs + 8 bytes of padding
-    static constexpr int EPI_BYTES = WAVES * 128 * PITCH;
+    static constexpr int EPI_BYTES = WAVES * WTM * PITCH;
     static constexpr int LDS_BYTES = EPI_BYTES > NS * STAGE_BYTES ? EPI_BYTES : NS * STAGE_BYTES;
     static constexpr int BPW = BM / RPB / WAVES;         // 1 KB blocks per wavefront per operand per stage
     static constexpr int LPW = 2 * BPW;                  // direct-to-LDS loads per wavefront per stage
+    static_assert(BM == BN && BPW * RPB * WAVES == BM, "A and W stages are filled by the same lanes");
+    static_assert(SUPER % BM == 0 && SUPER % BN == 0, "workgroup tiles divide the super tile");
     static_assert(NS >= 2 && NS <= 4 && LDS_BYTES <= 160 * 1024, "stage configuration");
 };
 
@@ -285,13 +297,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, lo
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Raw int32 store of one wavefront's 128 x (32 FN) block (test export only): straight from the fragment layout.
-template <int FN>
-__device__ __forceinline__ void store_tile_i32(const v16i (&acc)[4][FN], int* o, int M, int N, int mb, int nb,
+// Raw int32 store of one wavefront's (32 FM) x (32 FN) block (test export only): straight from the fragment layout.
+template <int FM, int FN>
+__device__ __forceinline__ void store_tile_i32(const v16i (&acc)[FM][FN], int* o, int M, int N, int mb, int nb,
                                                int lane) {
     const bool vec = (N & 3) == 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FM; ++i) {
         const int m = mb + i * 32 + (lane & 31);
         if (m >= M) continue;
 #pragma unroll
@@ -314,16 +326,16 @@ __device__ __forceinline__ void store_tile_i32(const v16i (&acc)[4][FN], int* o,
 
 // Epilogue through LDS: the fragment layout gives each lane 4 consecutive columns of one row, so global stores
 // straight from registers write 8-16 byte pieces of many cache lines (measured at a fraction of HBM write bandwidth).
-// Instead each wavefront writes its 128 x (32 FN) block of finished 16-bit values into its own LDS region (rows
+// Instead each wavefront writes its (32 FM) x (32 FN) block of finished 16-bit values into its own LDS region (rows
 // padded by 8 bytes: the 8-byte writes of consecutive lanes fall on distinct banks), then reads it back row-major and
-// stores whole 128-byte lines.
-template <typename T, int EPI, int FN, int PITCH>
-__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][FN], uint8_t* eb, void* out, const float* sa,
+// stores whole lines.
+template <typename T, int EPI, int FM, int FN, int PITCH>
+__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_t* eb, void* out, const float* sa,
                                                const float* sw, const uint16_t* bias, int M, int N, int sa_rows,
                                                int sw_rows, int mb, int nb, int lane) {
-    float sam[4];
+    float sam[FM];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sam[i] = sa[sa_rows ? min(mb + i * 32 + (lane & 31), M - 1) : 0];
+    for (int i = 0; i < FM; ++i) sam[i] = sa[sa_rows ? min(mb + i * 32 + (lane & 31), M - 1) : 0];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -353,7 +365,7 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][FN], uint8_t
                 }
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < FM; ++i) {
                 const int ml = i * 32 + (lane & 31);
                 uint16_t h[4];
 #pragma unroll
@@ -378,7 +390,7 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][FN], uint8_t
     const bool vec = (N & 7) == 0;
     uint16_t* o = static_cast<uint16_t*>(out);
 #pragma unroll 4
-    for (int it = 0; it < 128 / RPI; ++it) {
+    for (int it = 0; it < 32 * FM / RPI; ++it) {
         const int rl = it * RPI + lane / LPR, cl = (lane % LPR) * 8;
         const int m = mb + rl, n = nb + cl;
         const uint2 lo = *reinterpret_cast<const uint2*>(eb + rl * PITCH + cl * 2);
@@ -414,30 +426,31 @@ __device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rsa, __amdgpu_b
     }
 }
 
-// Block of 2 * WN wavefronts (WN = 4: two per SIMD, so one wavefront's LDS and barrier waits are covered by the
-// other's MFMAs).
-template <typename T, int EPI, int WN, int KB, int NS, int GM = GROUP_M, bool PRIO = false>
-__global__ void __launch_bounds__(128 * WN) gemm_kernel(const int8_t* __restrict__ a,
-                                                                    const int8_t* __restrict__ w,
-                                                                    const float* __restrict__ sa,
-                                                                    const float* __restrict__ sw,
-                                                                    const uint16_t* __restrict__ bias,
-                                                                    void* __restrict__ out, int M, int N, int K,
-                                                                    int sa_rows, int sw_rows) {
-    // (GemmCfg<WN, KB, NS>:: spelled out: a local alias of it used inside the lambdas below silently drops the kernel's
-    // host-side stub)
+// WM x WN wavefronts (main configuration 2 x 4: two per SIMD, so one wavefront's LDS and barrier waits are covered by
+// the other's MFMAs).  Workgroup u of the grid computes quarter (or whole) tile u % SUB of super tile t_base + u / SUB.
+template <typename T, int EPI, int WM, int WN, int FM, int FN, int KB, int NS, int GM = GROUP_M, bool PRIO = false>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                            const float* __restrict__ sa, const float* __restrict__ sw,
+                                                            const uint16_t* __restrict__ bias, void* __restrict__ out,
+                                                            int M, int N, int K, int sa_rows, int sw_rows, int t_base) {
     extern __shared__ v4i ldsx[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    using Cfg = GemmCfg<WM, WN, FM, FN, KB, NS>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, SUB = Cfg::SUB, WTM = 32 * FM, WTN = 32 * FN;
+    constexpr int PITCH = WTN * 2 + 8;
 
-    // XCD-aware remap: hardware places block b on XCD b % 8; give each XCD a contiguous run of tiles
-    const int TM = (M + BM - 1) / BM, TN = (N + BN - 1) / BN;
+    // XCD-aware remap: hardware places workgroup b on XCD b % 8; give each XCD a contiguous run of tiles (and the
+    // SUB quarters of one super tile to the same XCD)
+    const int TM = (M + SUPER - 1) / SUPER, TN = (N + SUPER - 1) / SUPER;
     const int nb = gridDim.x, per = nb >> 3;
-    int b = blockIdx.x;
-    if (b < per * 8) b = (b & 7) * per + (b >> 3);
-    const int gsz = GM * TN, grp = b / gsz, first_m = grp * GM;
+    int u = blockIdx.x;
+    if (u < per * 8) u = (u & 7) * per + (u >> 3);
+    const int t = t_base + u / SUB, q = u % SUB;
+    const int gsz = GM * TN, grp = t / gsz, first_m = grp * GM;
     const int gm = min(TM - first_m, GM);
-    const int tm = first_m + (b % gsz) % gm, tn = (b % gsz) / gm;
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
+    const int m0 = tm * SUPER + (q / (SUPER / BN)) * BM, n0 = tn * SUPER + (q % (SUPER / BN)) * BN;
+    if (m0 >= M || n0 >= N) return;                      // a quarter past the edge of the last super tile (uniform)
 
     // global -> LDS directly (buffer_load_dwordx4 ... lds): one wavefront instruction fills 1 KB of LDS, i.e.
     // 1024 / KB rows of one stage; lane l lands at byte 16 l of it, so it fetches the logical chunk that the swizzle
@@ -445,7 +458,6 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(const int8_t* __restrict
     // stage s is computed, so no register holds staged data and the memory latency has NS - 1 stages of MFMA
     // work to hide behind.
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
-    using Cfg = GemmCfg<WN, KB, NS>;
     constexpr int CPR = Cfg::CPR, BPW = Cfg::BPW;
     const int drow = lane / CPR, pch = lane % CPR;       // row within the 1 KB block; physical chunk position
     int oa[BPW], ow[BPW], ch[BPW];
@@ -462,28 +474,28 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(const int8_t* __restrict
     };
 
     const int wm = wave / WN, wn = wave % WN;
-    v16i acc[4][GemmCfg<WN, KB, NS>::FN];
+    v16i acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < GemmCfg<WN, KB, NS>::FN; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
     auto compute = [&](int stage) {
         const v4i* la = reinterpret_cast<const v4i*>(lbase + stage * Cfg::STAGE_BYTES);
         const v4i* lw = la + BM * CPR;
-        v4i fa[2][4], fw[2][Cfg::FN];
+        v4i fa[2][FM], fw[2][FN];
         auto fload = [&](int sub, int fb) {
             const int cc = 2 * sub + (lane >> 5);        // this lane's 16-byte chunk of the staged row
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = wm * 128 + i * 32 + (lane & 31);
+            for (int i = 0; i < FM; ++i) {
+                const int row = wm * WTM + i * 32 + (lane & 31);
                 fa[fb][i] = la[row * CPR + (cc ^ swz<CPR>(row))];
             }
 #pragma unroll
-            for (int j = 0; j < Cfg::FN; ++j) {
-                const int row = wn * Cfg::WTN + j * 32 + (lane & 31);
+            for (int j = 0; j < FN; ++j) {
+                const int row = wn * WTN + j * 32 + (lane & 31);
                 fw[fb][j] = lw[row * CPR + (cc ^ swz<CPR>(row))];
             }
         };
@@ -497,9 +509,9 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(const int8_t* __restrict
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);   // favour the wavefront issuing MFMAs (measured neutral)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < Cfg::FN; ++j)
+                for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub & 1][j], fa[sub & 1][i], acc[i][j], 0, 0,
                                                                       0);
             if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
@@ -527,13 +539,13 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(const int8_t* __restrict
 
     // D fragment of v_mfma_i32_32x32x32_i8 with the weights as the A operand: lane holds column lane % 32 of the
     // 32 x 32 block (activation row m) and its rows 8 q + 4 (lane / 32) + r, q, r = 0..3 (weight rows n).
-    const int mb = m0 + wm * 128, nbw = n0 + wn * GemmCfg<WN, KB, NS>::WTN;
+    const int mb = m0 + wm * WTM, nbw = n0 + wn * WTN;
     if constexpr (EPI == EPI_I32) {
-        store_tile_i32<GemmCfg<WN, KB, NS>::FN>(acc, static_cast<int*>(out), M, N, mb, nbw, lane);
+        store_tile_i32<FM, FN>(acc, static_cast<int*>(out), M, N, mb, nbw, lane);
     } else {
         __syncthreads();                                 // every wavefront is done reading the K stages
-        store_tile_lds<T, EPI, GemmCfg<WN, KB, NS>::FN, GemmCfg<WN, KB, NS>::PITCH>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * 128 * GemmCfg<WN, KB, NS>::PITCH, out,
-                                                sa, sw, bias, M, N, sa_rows, sw_rows, mb, nbw, lane);
+        store_tile_lds<T, EPI, FM, FN, PITCH>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * WTM * PITCH, out, sa, sw,
+                                              bias, M, N, sa_rows, sw_rows, mb, nbw, lane);
     }
 }
 
@@ -595,19 +607,61 @@ static void launch_stream(const Args& p) {
     else launch_stream_cfg<T, 2, 4, 4, 4, EPI, false>(p);
 }
 
-// 8 wavefronts, 128-byte K stages, 2 in LDS: measured ~9% faster than 64-byte stages x 4 at every prefill shape (half
-// the barriers outweigh the shorter prefetch distance)
-constexpr int GEMM_WN = 4, GEMM_KB = 128, GEMM_NS = 2;
+// Main configuration: 256 x 256 tiles, 2 x 4 wavefronts of 128 x 64, 128-byte K stages, 2 in LDS (128 KB): measured
+// ~9% faster than 64-byte stages x 4 at every prefill shape (half the barriers outweigh the shorter prefetch distance).
+// Small configuration: 128 x 128 quarter tiles, 2 x 2 wavefronts of 64 x 64, the same stages (64 KB: two workgroups
+// per CU).
+struct MainCfg { static constexpr int WM = 2, WN = 4, FM = 4, FN = 2, KB = 128, NS = 2; };
+struct SmallCfg { static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128, NS = 2; };
 
-template <typename T, int EPI, int WN = GEMM_WN, int KB = GEMM_KB, int NS = GEMM_NS>
-static void launch_gemm(const Args& p) {
-    using C = GemmCfg<WN, KB, NS>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, EPI, WN, KB, NS>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+// Which configuration covers which super tiles: 0 = main only, 2 = small only, 1 = main for the whole rounds of super
+// tiles over the CUs and small for a last partial round of at most CUs / W8_SMALL_REM_DIV super tiles.
+#ifndef W8_GEMM_POLICY
+#define W8_GEMM_POLICY 1
+#endif
+#ifndef W8_SMALL_REM_DIV
+#define W8_SMALL_REM_DIV 2
+#endif
+
+template <typename T, int EPI, typename C>
+static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
+    using G = GemmCfg<C::WM, C::WN, C::FM, C::FN, C::KB, C::NS>;
+    const void* kern = reinterpret_cast<const void*>(&gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS>);
+    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
     (void)attr;
-    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    gemm_kernel<T, EPI, WN, KB, NS><<<tiles, C::THREADS, C::LDS_BYTES, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
-                                                                               p.M, p.N, p.K, p.sa_rows, p.sw_rows);
+    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
+        p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
+}
+
+// Compute units of the current device (cached per device).
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev] = v;
+    }
+    return cached[dev];
+}
+
+template <typename T, int EPI>
+static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
+    const int tiles = ((p.M + SUPER - 1) / SUPER) * ((p.N + SUPER - 1) / SUPER);
+    constexpr int SUB = GemmCfg<SmallCfg::WM, SmallCfg::WN, SmallCfg::FM, SmallCfg::FN, SmallCfg::KB, SmallCfg::NS>::SUB;
+    if (policy == 2) {
+        launch_gemm_cfg<T, EPI, SmallCfg>(p, 0, tiles * SUB);
+        return;
+    }
+    const int cus = cu_count();
+    const int full = tiles / cus * cus, rem = tiles - full;
+    if (policy == 0 || rem == 0 || rem > cus / W8_SMALL_REM_DIV) {
+        launch_gemm_cfg<T, EPI, MainCfg>(p, 0, tiles);
+        return;
+    }
+    if (full > 0) launch_gemm_cfg<T, EPI, MainCfg>(p, 0, full);
+    launch_gemm_cfg<T, EPI, SmallCfg>(p, full, rem * SUB);
 }
 
 template <int EPI>
@@ -687,10 +741,11 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 }
 
 // Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
-// M <= 32; kernel 1 = the prefill kernel; kernel 2 = the VALU dot4 kernel, M <= 2, K <= 8192).  Returns -1 on bad
+// M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M <= 2, K <= 8192; kernel 3
+// = the prefill kernel's small configuration alone; kernel 4 = its main configuration alone).  Returns -1 on bad
 // arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
-    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 2) return -1;
+    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 4) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
                  (hipStream_t)stream};
     if (kernel == 0) {
@@ -699,6 +754,10 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
         else launch_stream_cfg<f16, 2, 4, 4, 4, EPI_I32, false>(p);
     } else if (kernel == 1) {
         launch_gemm<f16, EPI_I32>(p);
+    } else if (kernel == 3) {
+        launch_gemm<f16, EPI_I32>(p, 2);
+    } else if (kernel == 4) {
+        launch_gemm<f16, EPI_I32>(p, 0);
     } else {
         if (!dot4_ok(p)) return -1;
         launch_dot4<f16, EPI_I32>(p);
