@@ -188,7 +188,8 @@ def test_i32_stream_kernel(L, M, N, K):
 
 
 DOT4_SHAPES = [(1, 17408, 5120), (2, 17408, 5120), (1, 1000, 5136), (2, 300, 16), (1, 64, 8192), (2, 33, 48),
-               (1, 7, 1040)]
+               (1, 7, 1040), (1, 5120, 17408), (2, 300, 17408), (1, 129, 9232), (2, 64, 12304), (3, 17408, 5120),
+               (3, 100, 8192), (3, 5, 16)]
 
 
 @pytest.mark.parametrize("M,N,K", DOT4_SHAPES)
@@ -231,8 +232,8 @@ def test_i32_extreme_values(L):
     a = torch.full((40, K), -128, dtype=torch.int8)
     w = torch.full((64, K), -128, dtype=torch.int8)
     w[1::2] = 127
-    for kernel, aa, ww in ((0, a[:8], w), (1, a, w), (3, a, w), (2, a[:2, :8192].contiguous(),
-                                                                w[:, :8192].contiguous())):
+    for kernel, aa, ww in ((0, a[:8], w), (1, a, w), (3, a, w), (2, a[:2], w),
+                           (2, a[:3, :8192].contiguous(), w[:, :8192].contiguous())):
         got = i32(L, aa.to(DEV), ww.to(DEV), kernel)
         assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), ww.numpy()))
 
@@ -249,6 +250,8 @@ def run_scaled_mm(a, w, sa, sw, bias, dt):
 CASES = [
     # M, N, K, dtype, bias, per-tensor sa, expected epilogue order
     (1, 17408, 5120, torch.float16, False, False, 0),      # decode GEMV
+    (1, 5120, 17408, torch.bfloat16, True, False, 0),      # VALU kernel at K = 17408
+    (3, 5120, 8192, torch.float16, False, True, 0),        # VALU kernel with three rows
     (4, 7168, 5120, torch.bfloat16, True, False, 0),
     (8, 5120, 8704, torch.float16, False, True, 0),
     (12, 1000, 5136, torch.float16, True, False, 0),

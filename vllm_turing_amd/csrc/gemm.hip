@@ -12,7 +12,7 @@
 //    128-byte line per row per step) and feeds v_mfma_i32_16x16x64_i8 with the weights as the A operand and up to 16
 //    activation rows per MFMA as the B operand, so the int8 dot products never touch the VALU.  The K slices of a
 //    tile meet in LDS.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
-//  * gemv_dot4_kernel, M <= 2 and K <= 8192 (decode): weight-streaming through the VALU: each wavefront instruction
+//  * gemv_dot4_kernel, M <= 2 and K <= 17408, or M = 3 and K <= 8192 (decode): weight-streaming through the VALU: each wavefront instruction
 //    reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in registers, wavefront
 //    reduction with DPP / ds_swizzle.  Small-M epilogue chain.
 //  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
@@ -572,30 +572,47 @@ static void launch_stream_cfg(const Args& p) {
                                                                p.sa_rows, p.sw_rows);
 }
 
-// Decode with one or two activation rows: the VALU kernel, one wavefront per two weight rows (measured fastest for
-// K = 5120, N = 17408: every wavefront issues its loads at once and the whole grid is resident).
-constexpr int DOT4_MAX_M = 2, DOT4_MAX_CH = 8;           // K <= 64 * 16 * 8 = 8192
+// Decode with few activation rows: the VALU kernel, one wavefront per two weight rows (measured fastest for
+// K = 5120, N = 17408: every wavefront issues its loads at once and the whole grid is resident; also for K = 17408 at
+// one or two rows (18.2 vs 25.1 us at N = 5120) and for three rows at K <= 8192).  Chunk counts are rounded up to the
+// next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
+constexpr int DOT4_MAX_M = 3, DOT4_MAX_CH = 17, DOT4_MAX_CH_M3 = 8;
+
+static int dot4_chunks(int K) {
+    const int c = (K / 16 + 63) / 64;
+    return c <= 8 ? c : c <= 10 ? 10 : c <= 12 ? 12 : c <= 14 ? 14 : c <= 17 ? 17 : 1 << 20;
+}
 
 template <typename T, int M, int CH, int EPI>
 static void launch_dot4_ch(const Args& p) {
-    const int waves = (p.N + 1) / 2;
-    gemv_dot4_kernel<T, M, CH, 1, EPI><<<(waves + 3) / 4, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N,
-                                                                            p.K, p.sa_rows, p.sw_rows);
+    if constexpr (CH <= DOT4_MAX_CH && (M < 3 || CH <= DOT4_MAX_CH_M3)) {
+        const int waves = (p.N + 1) / 2;
+        gemv_dot4_kernel<T, M, CH, 1, EPI><<<(waves + 3) / 4, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
+                                                                                p.N, p.K, p.sa_rows, p.sw_rows);
+    }
 }
 template <typename T, int M, int EPI>
 static void launch_dot4_m(const Args& p) {
-    switch ((p.K / 16 + 63) / 64) {
+    if constexpr (M <= DOT4_MAX_M) {
+        switch (dot4_chunks(p.K)) {
 #define W8_CASE(C) case C: launch_dot4_ch<T, M, C, EPI>(p); break;
-        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8)
+            W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8) W8_CASE(10)
+            W8_CASE(12) W8_CASE(14) W8_CASE(17)
 #undef W8_CASE
+        }
     }
 }
-static bool dot4_ok(const Args& p) { return p.M <= DOT4_MAX_M && p.K <= 64 * 16 * DOT4_MAX_CH; }
+static bool dot4_ok(const Args& p) {
+    return p.M <= DOT4_MAX_M && dot4_chunks(p.K) <= (p.M < 3 ? DOT4_MAX_CH : DOT4_MAX_CH_M3);
+}
 
 template <typename T, int EPI>
 static void launch_dot4(const Args& p) {
-    if (p.M == 1) launch_dot4_m<T, 1, EPI>(p);
-    else launch_dot4_m<T, 2, EPI>(p);
+    switch (p.M) {
+        case 1: launch_dot4_m<T, 1, EPI>(p); break;
+        case 2: launch_dot4_m<T, 2, EPI>(p); break;
+        case 3: launch_dot4_m<T, 3, EPI>(p); break;
+    }
 }
 
 // M <= 32: the VALU kernel where it applies, else the MFMA streaming kernel (K split 4 ways per 16-row tile, 4 steps
@@ -741,7 +758,8 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 }
 
 // Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
-// M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M <= 2, K <= 8192; kernel 3
+// M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M <= 2 and K <= 17408 or
+// M = 3 and K <= 8192; kernel 3
 // = the prefill kernel's small configuration alone; kernel 4 = its main configuration alone).  Returns -1 on bad
 // arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
