@@ -203,6 +203,21 @@ def test_i32_dot4_kernel(L, M, N, K):
     assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
 
 
+DOT4L_SHAPES = [(3, 17408, 5120), (4, 17408, 5120), (8, 17408, 5120), (4, 5120, 17408), (5, 5120, 12304), (8, 300, 9216),
+                (6, 7, 16), (7, 1001, 5136), (3, 64, 24576)]
+
+
+@pytest.mark.parametrize("M,N,K", DOT4L_SHAPES)
+def test_i32_dot4_lds_kernel(L, M, N, K):
+    say(f"i32 dot4 lds M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 19 + N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    got = i32(L, a.to(DEV), w.to(DEV), 5)
+    ref = oracle.gemm_i32(a.numpy(), w.numpy())
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+
+
 GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80), (97, 272, 5120),
                (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248), (4096, 256, 17408)]
 
@@ -233,7 +248,7 @@ def test_i32_extreme_values(L):
     w = torch.full((64, K), -128, dtype=torch.int8)
     w[1::2] = 127
     for kernel, aa, ww in ((0, a[:8], w), (1, a, w), (3, a, w), (2, a[:2], w),
-                           (2, a[:3, :8192].contiguous(), w[:, :8192].contiguous())):
+                           (2, a[:3, :8192].contiguous(), w[:, :8192].contiguous()), (5, a[:4], w)):
         got = i32(L, aa.to(DEV), ww.to(DEV), kernel)
         assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), ww.numpy()))
 

@@ -6,7 +6,7 @@
 // it, passed to cutlass_scaled_mm as its [K, N] stride-(1, K) view); sa: float32 [M] or [1]; sw: float32 [N] or [1];
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
-// Three kernels:
+// Four kernels:
 //  * stream_kernel, M <= 32 (decode and speculative verify): weight-streaming and HBM-bound.  Every wavefront owns
 //    16 weight rows and a slice of K, reads each weight byte exactly once with 16-byte non-temporal loads (a full
 //    128-byte line per row per step) and feeds v_mfma_i32_16x16x64_i8 with the weights as the A operand and up to 16
@@ -15,6 +15,8 @@
 //  * gemv_dot4_kernel, M <= 2 and K <= 17408, or M = 3 and K <= 8192 (decode): weight-streaming through the VALU: each wavefront instruction
 //    reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in registers, wavefront
 //    reduction with DPP / ds_swizzle.  Small-M epilogue chain.
+//  * gemv_dot4_lds_kernel, M = 3 or 4 and K > 8192 (decode of the long-K down projection): the same with the
+//    activations copied once per workgroup into LDS instead of into every wavefront's registers.
 //  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
 //    each a 4 x 2 grid of v_mfma_i32_32x32x32_i8; 128-byte K stages loaded straight from HBM into LDS
 //    (buffer_load ... lds), double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128
@@ -24,7 +26,7 @@
 //    64 x 64, two workgroups per CU) so it spreads over the whole chip.  The epilogue goes through LDS so that every
 //    global store writes whole lines.  Large-M epilogue (csrc/w8a8_big.cu:26-35).
 //
-// Both kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
+// The kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
 // MFMA the same permutation of k on its A and B operands, so every operand load is a contiguous 16-byte vector.
 // Integer accumulation is exact (|acc| < 2^31 for K < 131072), so split-K order and tile order are free and the int32
 // results are bit-exact.
@@ -243,6 +245,83 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
         finish(1, n0);
         n0 += stride;
         if (n0 >= N) break;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// gemv_dot4_lds_kernel: 3..8 activation rows staged once per workgroup in LDS, weights streamed once through the VALU
+// ---------------------------------------------------------------------------------------------------------------------
+// With more than two rows, activations held in every wavefront's registers cost more L2 traffic than the weights
+// themselves (each wavefront reloads all of [M, K]) and limit occupancy; here the workgroup copies [M, K] into LDS
+// once and every wavefront reads the chunk it needs next to each weight chunk.  A wavefront walks its weight rows
+// (wid, wid + nw, ...) in groups of G 1 KB chunks (lane l owns 16-byte chunk l of each 1 KB), the next group's loads
+// issued before this group's v_dot4 math; a row's per-lane sums are reduced across the wavefront once the row ends.
+template <typename T, int M, int G, int EPI>
+__global__ void __launch_bounds__(512) gemv_dot4_lds_kernel(const int8_t* __restrict__ a,
+                                                            const int8_t* __restrict__ w,
+                                                            const float* __restrict__ sa,
+                                                            const float* __restrict__ sw,
+                                                            const uint16_t* __restrict__ bias,
+                                                            void* __restrict__ out, int N, int K, int sa_rows,
+                                                            int sw_rows) {
+    extern __shared__ v4i act[];                         // [M][K / 16] chunks of 16 bytes
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (blockDim.x >> 6);
+    const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int K16 = K >> 4;
+    const int NG = ((K16 + 63) / 64 + G - 1) / G;        // chunk groups per row
+    const int nrows = wid < N ? (N - 1 - wid) / nw + 1 : 0;
+    const int items = nrows * NG;                        // (row, group) pairs of this wavefront
+    const v4i z = {0, 0, 0, 0};
+    v4i wb[2][G];
+    auto load = [&](int buf, int it) {
+        const int n = wid + (it / NG) * nw, g = it % NG;
+        const int8_t* row = w + (long)n * K;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int c = lane + 64 * (g * G + j);
+            wb[buf][j] = c < K16 ? wload<false>(row + c * 16) : z;
+        }
+    };
+    if (items > 0) load(0, 0);                           // the first weights are in flight during the staging
+    const v4i* a4 = reinterpret_cast<const v4i*>(a);
+    for (int i = threadIdx.x; i < M * K16; i += blockDim.x) act[i] = a4[i];
+    __syncthreads();
+
+    int s[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) s[m] = 0;
+    auto step = [&](int buf, int it) {
+        const int g = it % NG;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int c = min(lane + 64 * (g * G + j), K16 - 1);   // past K the weights are zero
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const v4i av = act[m * K16 + c];
+                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].x, av.x, s[m], false);
+                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].y, av.y, s[m], false);
+                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].z, av.z, s[m], false);
+                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].w, av.w, s[m], false);
+            }
+        }
+        if (g == NG - 1) {                               // row done: reduce, lane m writes output (m, n)
+            const int n = wid + (it / NG) * nw;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const int r = wave_sum(s[m]);
+                if (lane == m) store_out<T, EPI>(out, (long)m * N + n, r, sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
+                s[m] = 0;
+            }
+        }
+    };
+    // ping-pong with compile-time buffer indices
+    for (int it = 0; it < items; it += 2) {
+        if (it + 1 < items) load(1, it + 1);
+        step(0, it);
+        if (it + 1 >= items) break;
+        if (it + 2 < items) load(0, it + 2);
+        step(1, it + 1);
     }
 }
 
@@ -615,11 +694,43 @@ static void launch_dot4(const Args& p) {
     }
 }
 
+// 3..8 rows with [M, K] staged in LDS (at most DOT4L_MAX_BYTES, two workgroups of 8 wavefronts per CU).  Dispatched
+// for 3 or 4 rows with K > 8192 only, where it beats the MFMA streaming kernel (K = 17408, N = 5120: 22.2 / 24.2 vs
+// 26.1 / 26.9 us); with more rows or shorter K its M LDS reads per weight chunk make it slower.
+constexpr int DOT4L_G = 4;                               // 1 KB weight chunks per group (2 and 8 measured slower)
+constexpr int DOT4L_MIN_M = 3, DOT4L_MAX_M = 8, DOT4L_MAX_BYTES = 72 * 1024;
+static bool dot4l_ok(const Args& p) {
+    return p.M >= DOT4L_MIN_M && p.M <= DOT4L_MAX_M && (long)p.M * p.K <= DOT4L_MAX_BYTES;
+}
+static bool dot4l_pick(const Args& p) { return dot4l_ok(p) && p.M <= 4 && p.K > 8192; }
+template <typename T, int M, int EPI>
+static void launch_dot4l_m(const Args& p) {
+    const void* kern = reinterpret_cast<const void*>(&gemv_dot4_lds_kernel<T, M, DOT4L_G, EPI>);
+    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       DOT4L_MAX_BYTES);
+    (void)attr;
+    const int waves = (p.N + 1) / 2;
+    gemv_dot4_lds_kernel<T, M, DOT4L_G, EPI><<<(waves + 7) / 8, 512, M * p.K, p.st>>>(
+        p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
+}
+template <typename T, int EPI>
+static void launch_dot4l(const Args& p) {
+    switch (p.M) {
+        case 3: launch_dot4l_m<T, 3, EPI>(p); break;
+        case 4: launch_dot4l_m<T, 4, EPI>(p); break;
+        case 5: launch_dot4l_m<T, 5, EPI>(p); break;
+        case 6: launch_dot4l_m<T, 6, EPI>(p); break;
+        case 7: launch_dot4l_m<T, 7, EPI>(p); break;
+        case 8: launch_dot4l_m<T, 8, EPI>(p); break;
+    }
+}
+
 // M <= 32: the VALU kernel where it applies, else the MFMA streaming kernel (K split 4 ways per 16-row tile, 4 steps
 // of 128 bytes in flight per buffer; plain loads measured faster than non-temporal ones here).
 template <typename T, int EPI>
 static void launch_stream(const Args& p) {
     if (dot4_ok(p)) launch_dot4<T, EPI>(p);
+    else if (dot4l_pick(p)) launch_dot4l<T, EPI>(p);
     else if (p.M <= 16) launch_stream_cfg<T, 1, 4, 4, 4, EPI, false>(p);
     else launch_stream_cfg<T, 2, 4, 4, 4, EPI, false>(p);
 }
@@ -760,10 +871,10 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 // Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
 // M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M <= 2 and K <= 17408 or
 // M = 3 and K <= 8192; kernel 3
-// = the prefill kernel's small configuration alone; kernel 4 = its main configuration alone).  Returns -1 on bad
-// arguments, else the launch error.
+// = the prefill kernel's small configuration alone; kernel 4 = its main configuration alone; kernel 5 = the VALU
+// kernel with activations in LDS, 3 <= M <= 8, M * K <= 73728).  Returns -1 on bad arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
-    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 4) return -1;
+    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 5) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
                  (hipStream_t)stream};
     if (kernel == 0) {
@@ -776,6 +887,9 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
         launch_gemm<f16, EPI_I32>(p, 2);
     } else if (kernel == 4) {
         launch_gemm<f16, EPI_I32>(p, 0);
+    } else if (kernel == 5) {
+        if (!dot4l_ok(p)) return -1;
+        launch_dot4l<f16, EPI_I32>(p);
     } else {
         if (!dot4_ok(p)) return -1;
         launch_dot4<f16, EPI_I32>(p);
