@@ -57,9 +57,11 @@ int silu_mul_quant(const void* gu, void* q, void* scales, int M, int I, void* st
 /* The same for bfloat16 activations.  No counterpart in the reference (its kernel is fp16 only); same codes. */
 int silu_mul_quant_bf16(const void* gu, void* q, void* scales, int M, int I, void* stream);
 
-/* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop (kernel 0: the small-M
- * streaming kernel, M <= 32; kernel 1: the prefill kernel), for bit-exact accumulator checks.  No counterpart in the
- * reference.  Returns -1 on bad arguments, else the HIP launch error. */
+/* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
+ * checks: kernel 0 the small-M MFMA streaming kernel (M <= 32), 1 the prefill kernel as dispatched, 2 the v_dot4
+ * streaming kernel (M = 1 and K <= 17408, or M = 2 and K <= 8192), 3 and 4 the prefill kernel's quarter-tile and
+ * full-tile configurations alone.  No counterpart in the reference.  Returns -1 on bad arguments, else the HIP launch
+ * error. */
 int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream);
 
 /* Test export: the device silu of all 65,536 input patterns of dtype, out[65536] uint16 bit patterns.  No

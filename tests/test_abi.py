@@ -58,12 +58,10 @@ def test_argument_validation_codes(L):
     assert L.w8a8_big(16, 16, 0, 0, 0, 64, 64, 72, 0, None) == 1                  # K % 16
     assert L.w8a8_scaled_mm(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
     assert L.w8a8_i32(16, 16, 0, 33, 64, 64, 0, None) == -1                       # streaming kernel: M <= 32
-    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 2, None) == -1                       # VALU kernel: M <= 3
-    assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # VALU kernel: K <= 17408
-    assert L.w8a8_i32(16, 16, 0, 3, 64, 8208, 2, None) == -1                     # and K <= 8192 at M = 3
-    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 6, None) == -1
-    assert L.w8a8_i32(16, 16, 0, 2, 64, 64, 5, None) == -1                       # LDS VALU kernel: 3 <= M <= 8
-    assert L.w8a8_i32(16, 16, 0, 8, 64, 9232, 5, None) == -1                     # and M * K <= 73728
+    assert L.w8a8_i32(16, 16, 0, 3, 64, 64, 2, None) == -1                       # VALU kernel: M <= 2
+    assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # K <= 17408 at one row
+    assert L.w8a8_i32(16, 16, 0, 2, 64, 8208, 2, None) == -1                     # K <= 8192 at two rows
+    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 5, None) == -1
     # silu_mul_quant: 1 = bad I, 0 for M == 0 (csrc/silu_quant.cu:72-73)
     assert L.silu_mul_quant(None, None, None, 4, 12, None) == 1
     assert L.silu_mul_quant(None, None, None, 0, 16, None) == 0

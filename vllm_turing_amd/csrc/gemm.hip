@@ -6,17 +6,15 @@
 // it, passed to cutlass_scaled_mm as its [K, N] stride-(1, K) view); sa: float32 [M] or [1]; sw: float32 [N] or [1];
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
-// Four kernels:
-//  * stream_kernel, M <= 32 (decode and speculative verify): weight-streaming and HBM-bound.  Every wavefront owns
-//    16 weight rows and a slice of K, reads each weight byte exactly once with 16-byte non-temporal loads (a full
-//    128-byte line per row per step) and feeds v_mfma_i32_16x16x64_i8 with the weights as the A operand and up to 16
-//    activation rows per MFMA as the B operand, so the int8 dot products never touch the VALU.  The K slices of a
-//    tile meet in LDS.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
-//  * gemv_dot4_kernel, M <= 2 and K <= 17408, or M = 3 and K <= 8192 (decode): weight-streaming through the VALU: each wavefront instruction
-//    reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in registers, wavefront
-//    reduction with DPP / ds_swizzle.  Small-M epilogue chain.
-//  * gemv_dot4_lds_kernel, M = 3 or 4 and K > 8192 (decode of the long-K down projection): the same with the
-//    activations copied once per workgroup into LDS instead of into every wavefront's registers.
+// Three kernels:
+//  * gemv_dot4_kernel, M = 1 and K <= 17408, or M = 2 and K <= 8192 (decode): weight-streaming through the VALU: each
+//    wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in
+//    registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
+//  * stream_lds_kernel, the rest of M <= 32 (decode, speculative verify): weight-streaming and HBM-bound.  A workgroup
+//    owns 16 weight rows; its 4 wavefronts take interleaved 128-byte K steps, each through a private LDS ring filled
+//    by direct-to-LDS loads of 1 KB (8 rows x 128 contiguous bytes each), and feed v_mfma_i32_16x16x64_i8 with the
+//    weights as the A operand and up to 16 activation rows per MFMA as the B operand.  The K slices of a tile meet in
+//    LDS.  Small-M epilogue chain.
 //  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
 //    each a 4 x 2 grid of v_mfma_i32_32x32x32_i8; 128-byte K stages loaded straight from HBM into LDS
 //    (buffer_load ... lds), double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128
@@ -27,7 +25,8 @@
 //    global store writes whole lines.  Large-M epilogue (csrc/w8a8_big.cu:26-35).
 //
 // The kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
-// MFMA the same permutation of k on its A and B operands, so every operand load is a contiguous 16-byte vector.
+// MFMA the same permutation of k on its A and B operands (the dot4 kernel pairs weight and activation chunks the
+// same way), so every operand is a contiguous 16-byte vector.
 // Integer accumulation is exact (|acc| < 2^31 for K < 131072), so split-K order and tile order are free and the int32
 // results are bit-exact.
 #include <type_traits>
@@ -62,109 +61,6 @@ template <bool NT>
 __device__ __forceinline__ v4i wload(const int8_t* p) {
     if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
     else return *reinterpret_cast<const v4i*>(p);
-}
-
-// ---------------------------------------------------------------------------------------------------------------------
-// stream_kernel: M <= 16 * MT rows, weights streamed once
-// ---------------------------------------------------------------------------------------------------------------------
-// Block = WPB wavefronts.  KS wavefronts split the K steps of one 16-row tile (interleaved 128-byte steps, so the
-// wavefronts of a tile read adjacent lines), WPB / KS tiles per block.  U steps of loads are kept in flight per
-// buffer, double-buffered.
-template <typename T, int MT, int KS, int U, int WPB, int EPI, bool NT = true>
-__global__ void __launch_bounds__(64 * WPB) stream_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
-                                                     const float* __restrict__ sa, const float* __restrict__ sw,
-                                                     const uint16_t* __restrict__ bias, void* __restrict__ out,
-                                                     int M, int N, int K, int sa_rows, int sw_rows) {
-    constexpr int TPB = WPB / KS;                        // tiles per block
-    __shared__ int red[KS > 1 ? TPB * (KS - 1) * MT * 4 * 64 : 1];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int ks = wave % KS, tl = wave / KS;
-    const int n0 = (blockIdx.x * TPB + tl) * 16;
-    const int r = lane & 15, g = lane >> 4;
-    const int8_t* wp = w + (long)min(n0 + r, N - 1) * K;
-    const int8_t* ap[MT];
-    bool av[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        av[mt] = mt * 16 + r < M;
-        ap[mt] = a + (long)min(mt * 16 + r, M - 1) * K;
-    }
-    v4i acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
-
-    const int nsteps = (K + 127) >> 7;
-    const v4i z = {0, 0, 0, 0};
-    v4i wb[2][U][2], ab[2][U][MT][2];
-    auto load = [&](int buf, int s0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int s = s0 + u * KS;
-            const int k = s * 128 + g * 32;
-            const bool ok0 = s < nsteps && k < K, ok1 = s < nsteps && k + 16 < K;
-            wb[buf][u][0] = ok0 ? wload<NT>(wp + k) : z;
-            wb[buf][u][1] = ok1 ? wload<NT>(wp + k + 16) : z;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                ab[buf][u][mt][0] = ok0 && av[mt] ? *reinterpret_cast<const v4i*>(ap[mt] + k) : z;
-                ab[buf][u][mt][1] = ok1 && av[mt] ? *reinterpret_cast<const v4i*>(ap[mt] + k + 16) : z;
-            }
-        }
-    };
-    auto compute = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wb[buf][u][0], ab[buf][u][mt][0], acc[mt], 0, 0, 0);
-                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wb[buf][u][1], ab[buf][u][mt][1], acc[mt], 0, 0, 0);
-            }
-        }
-    };
-    if (n0 < N) {
-        // ping-pong with compile-time buffer indices (keeps both buffers in registers)
-        int s0 = ks;
-        load(0, s0);
-        while (true) {
-            if (s0 + KS * U < nsteps) load(1, s0 + KS * U);
-            compute(0);
-            s0 += KS * U;
-            if (s0 >= nsteps) break;
-            if (s0 + KS * U < nsteps) load(0, s0 + KS * U);
-            compute(1);
-            s0 += KS * U;
-            if (s0 >= nsteps) break;
-        }
-    }
-    if constexpr (KS > 1) {
-        int* rb = red + (tl * (KS - 1)) * MT * 4 * 64 + lane;
-        if (ks > 0) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) rb[((ks - 1) * MT * 4 + mt * 4 + v) * 64] = acc[mt][v];
-        }
-        __syncthreads();
-        if (ks > 0) return;
-#pragma unroll
-        for (int q = 0; q < KS - 1; ++q)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[mt][v] += rb[(q * MT * 4 + mt * 4 + v) * 64];
-    }
-    if (n0 >= N) return;
-    // D fragment of v_mfma_i32_16x16x64_i8: lane holds rows 4 g + v (weight rows n) of column r (activation row m)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + r;
-        if (m >= M) continue;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = n0 + 4 * g + v;
-            if (n < N) store_out<T, EPI>(out, (long)m * N + n, acc[mt][v], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -245,83 +141,6 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
         finish(1, n0);
         n0 += stride;
         if (n0 >= N) break;
-    }
-}
-
-// ---------------------------------------------------------------------------------------------------------------------
-// gemv_dot4_lds_kernel: 3..8 activation rows staged once per workgroup in LDS, weights streamed once through the VALU
-// ---------------------------------------------------------------------------------------------------------------------
-// With more than two rows, activations held in every wavefront's registers cost more L2 traffic than the weights
-// themselves (each wavefront reloads all of [M, K]) and limit occupancy; here the workgroup copies [M, K] into LDS
-// once and every wavefront reads the chunk it needs next to each weight chunk.  A wavefront walks its weight rows
-// (wid, wid + nw, ...) in groups of G 1 KB chunks (lane l owns 16-byte chunk l of each 1 KB), the next group's loads
-// issued before this group's v_dot4 math; a row's per-lane sums are reduced across the wavefront once the row ends.
-template <typename T, int M, int G, int EPI>
-__global__ void __launch_bounds__(512) gemv_dot4_lds_kernel(const int8_t* __restrict__ a,
-                                                            const int8_t* __restrict__ w,
-                                                            const float* __restrict__ sa,
-                                                            const float* __restrict__ sw,
-                                                            const uint16_t* __restrict__ bias,
-                                                            void* __restrict__ out, int N, int K, int sa_rows,
-                                                            int sw_rows) {
-    extern __shared__ v4i act[];                         // [M][K / 16] chunks of 16 bytes
-    const int lane = threadIdx.x & 63;
-    const int nw = gridDim.x * (blockDim.x >> 6);
-    const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int K16 = K >> 4;
-    const int NG = ((K16 + 63) / 64 + G - 1) / G;        // chunk groups per row
-    const int nrows = wid < N ? (N - 1 - wid) / nw + 1 : 0;
-    const int items = nrows * NG;                        // (row, group) pairs of this wavefront
-    const v4i z = {0, 0, 0, 0};
-    v4i wb[2][G];
-    auto load = [&](int buf, int it) {
-        const int n = wid + (it / NG) * nw, g = it % NG;
-        const int8_t* row = w + (long)n * K;
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const int c = lane + 64 * (g * G + j);
-            wb[buf][j] = c < K16 ? wload<false>(row + c * 16) : z;
-        }
-    };
-    if (items > 0) load(0, 0);                           // the first weights are in flight during the staging
-    const v4i* a4 = reinterpret_cast<const v4i*>(a);
-    for (int i = threadIdx.x; i < M * K16; i += blockDim.x) act[i] = a4[i];
-    __syncthreads();
-
-    int s[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) s[m] = 0;
-    auto step = [&](int buf, int it) {
-        const int g = it % NG;
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const int c = min(lane + 64 * (g * G + j), K16 - 1);   // past K the weights are zero
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const v4i av = act[m * K16 + c];
-                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].x, av.x, s[m], false);
-                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].y, av.y, s[m], false);
-                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].z, av.z, s[m], false);
-                s[m] = __builtin_amdgcn_sdot4(wb[buf][j].w, av.w, s[m], false);
-            }
-        }
-        if (g == NG - 1) {                               // row done: reduce, lane m writes output (m, n)
-            const int n = wid + (it / NG) * nw;
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const int r = wave_sum(s[m]);
-                if (lane == m) store_out<T, EPI>(out, (long)m * N + n, r, sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
-                s[m] = 0;
-            }
-        }
-    };
-    // ping-pong with compile-time buffer indices
-    for (int it = 0; it < items; it += 2) {
-        if (it + 1 < items) load(1, it + 1);
-        step(0, it);
-        if (it + 1 >= items) break;
-        if (it + 2 < items) load(0, it + 2);
-        step(1, it + 1);
     }
 }
 
@@ -629,6 +448,114 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// stream_lds_kernel: M <= 16 * MT rows, weights streamed once through per-wavefront LDS rings
+// ---------------------------------------------------------------------------------------------------------------------
+// The MFMA operand layout wants 16 different weight rows in one load instruction, which the vector L1 serves with tag
+// conflicts.  Here every load is a direct-to-LDS buffer_load of 1 KB that covers 8 rows x 128 contiguous bytes, and
+// the fragments are read from LDS in the MFMA layout.  A workgroup is one 16-row weight tile; its 4 wavefronts take
+// interleaved 128-byte K steps, each through its own ring of NS step buffers (16 weight rows, then 16 MT activation
+// rows, each 128 bytes with the 8-chunk swizzle), so a wavefront only waits for its own loads and no barrier runs in
+// the main loop.  Activation rows past M and K chunks past K are loaded from outside the buffer, which writes zeros.
+__device__ __forceinline__ void dma_step(__amdgpu_buffer_rsrc_t rsw, __amdgpu_buffer_rsrc_t rsa, uint8_t* dst,
+                                         const int* off, const int* chk, int lps, int k0, int K) {
+#pragma unroll
+    for (int j = 0; j < lps; ++j) {
+        const bool ok = k0 + chk[j] * 16 < K;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(j < 2 ? rsw : rsa, (lds_void*)(dst + j * 1024), 16,
+                                                 ok ? off[j] : 0x7fffffff, k0, 0, 0);
+    }
+}
+
+template <typename T, int MT, int NS, int EPI>
+__global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                         const float* __restrict__ sa, const float* __restrict__ sw,
+                                                         const uint16_t* __restrict__ bias, void* __restrict__ out,
+                                                         int M, int N, int K, int sa_rows, int sw_rows) {
+    constexpr int KS = 4;                                // wavefronts per tile
+    constexpr int ROWS = 16 + 16 * MT;                   // staged rows per step
+    constexpr int STEP_BYTES = ROWS * 128;
+    constexpr int LPS = ROWS / 8;                        // 1 KB loads per step
+    extern __shared__ v4i ldsx[];
+    const int ks = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = blockIdx.x * 16;
+    uint8_t* const ring = reinterpret_cast<uint8_t*>(ldsx) + ks * NS * STEP_BYTES;
+    const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
+    int off[LPS], chk[LPS];
+#pragma unroll
+    for (int j = 0; j < LPS; ++j) {
+        const int row = j * 8 + (lane >> 3);             // staged row; lane % 8 is the physical chunk
+        chk[j] = (lane & 7) ^ swz<8>(row);
+        if (j < 2) off[j] = n0 + row < N ? (n0 + row) * K + chk[j] * 16 : 0x7fffffff;
+        else off[j] = row - 16 < M ? (row - 16) * K + chk[j] * 16 : 0x7fffffff;
+    }
+    const int nsteps = (K + 127) >> 7;
+    const int mine = ks < nsteps ? (nsteps - 1 - ks) / KS + 1 : 0;   // own steps ks, ks + KS, ...
+    auto issue = [&](int i) {
+        dma_step(rsw, rsa, ring + (i % NS) * STEP_BYTES, off, chk, LPS, (ks + i * KS) * 128, K);
+    };
+    v4i acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+    const int r = lane & 15, g = lane >> 4;
+    auto compute = [&](int slot) {
+        const v4i* st = reinterpret_cast<const v4i*>(ring + slot * STEP_BYTES);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int c = 4 * sub + g;                   // this lane's 16-byte chunk of the 128-byte step
+            const v4i fw = st[r * 8 + (c ^ swz<8>(r))];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int ra = 16 + 16 * mt + r;
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw, st[ra * 8 + (c ^ swz<8>(ra))], acc[mt], 0, 0, 0);
+            }
+        }
+    };
+    constexpr int WAIT2 = waitcnt_vm(2 * LPS), WAIT1 = waitcnt_vm(LPS), WAIT0 = waitcnt_vm(0);
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < mine) issue(i);
+    for (int i = 0; i < mine; ++i) {
+        // own step i has landed once at most the later steps' loads (LPS each) remain outstanding
+        const int ahead = min(mine - 1 - i, NS - 2);
+        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAIT1);
+        else __builtin_amdgcn_s_waitcnt(WAIT0);
+        // the slot of step i - 1, whose fragments this wavefront has already consumed
+        if (i + NS - 1 < mine) issue(i + NS - 1);
+        compute(i % NS);
+    }
+
+    // K slices meet in LDS (after every wavefront is done with its ring)
+    __syncthreads();
+    int* red = reinterpret_cast<int*>(ldsx) + lane;
+    if (ks > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[((ks - 1) * MT * 4 + mt * 4 + v) * 64] = acc[mt][v];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int q = 0; q < KS - 1; ++q)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[mt][v] += red[(q * MT * 4 + mt * 4 + v) * 64];
+    // D fragment of v_mfma_i32_16x16x64_i8: lane holds rows 4 g + v (weight rows n) of column r (activation row m)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int n = n0 + 4 * g + v;
+            if (n < N) store_out<T, EPI>(out, (long)m * N + n, acc[mt][v], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------------------------------
 struct Args {
@@ -642,20 +569,12 @@ struct Args {
     hipStream_t st;
 };
 
-template <typename T, int MT, int KS, int U, int WPB, int EPI, bool NT = true>
-static void launch_stream_cfg(const Args& p) {
-    constexpr int TPB = WPB / KS;
-    const int tiles = (p.N + 15) / 16;
-    const int blocks = (tiles + TPB - 1) / TPB;
-    stream_kernel<T, MT, KS, U, WPB, EPI, NT><<<blocks, 64 * WPB, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K,
-                                                               p.sa_rows, p.sw_rows);
-}
-
-// Decode with few activation rows: the VALU kernel, one wavefront per two weight rows (measured fastest for
-// K = 5120, N = 17408: every wavefront issues its loads at once and the whole grid is resident; also for K = 17408 at
-// one or two rows (18.2 vs 25.1 us at N = 5120) and for three rows at K <= 8192).  Chunk counts are rounded up to the
-// next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
-constexpr int DOT4_MAX_M = 3, DOT4_MAX_CH = 17, DOT4_MAX_CH_M3 = 8;
+// One or two activation rows: the VALU kernel, one wavefront per two weight rows (measured fastest for K = 5120,
+// N = 17408: 16.8 us against 18.1 for the LDS-ring MFMA kernel; every wavefront issues its loads at once and the
+// whole grid is resident), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two rows up to K = 8192 (past
+// that the LDS-ring kernel wins, 19.6 vs 22.0 us at K = 17408).  Chunk counts are rounded up to the next of 1..8, 10,
+// 12, 14, 17 (chunks past K are masked).
+constexpr int DOT4_MAX_M = 2, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8;
 
 static int dot4_chunks(int K) {
     const int c = (K / 16 + 63) / 64;
@@ -664,7 +583,7 @@ static int dot4_chunks(int K) {
 
 template <typename T, int M, int CH, int EPI>
 static void launch_dot4_ch(const Args& p) {
-    if constexpr (CH <= DOT4_MAX_CH && (M < 3 || CH <= DOT4_MAX_CH_M3)) {
+    if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2)) {
         const int waves = (p.N + 1) / 2;
         gemv_dot4_kernel<T, M, CH, 1, EPI><<<(waves + 3) / 4, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
                                                                                 p.N, p.K, p.sa_rows, p.sw_rows);
@@ -682,7 +601,7 @@ static void launch_dot4_m(const Args& p) {
     }
 }
 static bool dot4_ok(const Args& p) {
-    return p.M <= DOT4_MAX_M && dot4_chunks(p.K) <= (p.M < 3 ? DOT4_MAX_CH : DOT4_MAX_CH_M3);
+    return p.M <= DOT4_MAX_M && dot4_chunks(p.K) <= (p.M < 2 ? DOT4_MAX_CH : DOT4_MAX_CH_M2);
 }
 
 template <typename T, int EPI>
@@ -690,49 +609,30 @@ static void launch_dot4(const Args& p) {
     switch (p.M) {
         case 1: launch_dot4_m<T, 1, EPI>(p); break;
         case 2: launch_dot4_m<T, 2, EPI>(p); break;
-        case 3: launch_dot4_m<T, 3, EPI>(p); break;
     }
 }
 
-// 3..8 rows with [M, K] staged in LDS (at most DOT4L_MAX_BYTES, two workgroups of 8 wavefronts per CU).  Dispatched
-// for 3 or 4 rows with K > 8192 only, where it beats the MFMA streaming kernel (K = 17408, N = 5120: 22.2 / 24.2 vs
-// 26.1 / 26.9 us); with more rows or shorter K its M LDS reads per weight chunk make it slower.
-constexpr int DOT4L_G = 4;                               // 1 KB weight chunks per group (2 and 8 measured slower)
-constexpr int DOT4L_MIN_M = 3, DOT4L_MAX_M = 8, DOT4L_MAX_BYTES = 72 * 1024;
-static bool dot4l_ok(const Args& p) {
-    return p.M >= DOT4L_MIN_M && p.M <= DOT4L_MAX_M && (long)p.M * p.K <= DOT4L_MAX_BYTES;
-}
-static bool dot4l_pick(const Args& p) { return dot4l_ok(p) && p.M <= 4 && p.K > 8192; }
-template <typename T, int M, int EPI>
-static void launch_dot4l_m(const Args& p) {
-    const void* kern = reinterpret_cast<const void*>(&gemv_dot4_lds_kernel<T, M, DOT4L_G, EPI>);
-    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       DOT4L_MAX_BYTES);
+// M <= 32 past the VALU kernel: the MFMA kernel through per-wavefront LDS rings of 3 steps (48 or 72 KB per
+// workgroup: three or two workgroups per CU); measured against 2 and 4 steps, and against loads straight into
+// registers (the LDS rings take M = 8, K = 5120, N = 17408 from 23.6 to 18.9 us and M = 32 from 45.6 to 28.1 us).
+constexpr int SLDS_NS = 3;
+template <typename T, int MT, int EPI>
+static void launch_stream_lds(const Args& p) {
+    constexpr int LDS = 4 * SLDS_NS * (16 + 16 * MT) * 128;
+    static_assert(LDS <= 160 * 1024, "LDS ring size");
+    const void* kern = reinterpret_cast<const void*>(&stream_lds_kernel<T, MT, SLDS_NS, EPI>);
+    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
     (void)attr;
-    const int waves = (p.N + 1) / 2;
-    gemv_dot4_lds_kernel<T, M, DOT4L_G, EPI><<<(waves + 7) / 8, 512, M * p.K, p.st>>>(
-        p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
-}
-template <typename T, int EPI>
-static void launch_dot4l(const Args& p) {
-    switch (p.M) {
-        case 3: launch_dot4l_m<T, 3, EPI>(p); break;
-        case 4: launch_dot4l_m<T, 4, EPI>(p); break;
-        case 5: launch_dot4l_m<T, 5, EPI>(p); break;
-        case 6: launch_dot4l_m<T, 6, EPI>(p); break;
-        case 7: launch_dot4l_m<T, 7, EPI>(p); break;
-        case 8: launch_dot4l_m<T, 8, EPI>(p); break;
-    }
+    stream_lds_kernel<T, MT, SLDS_NS, EPI><<<(p.N + 15) / 16, 256, LDS, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
+                                                                               p.M, p.N, p.K, p.sa_rows, p.sw_rows);
 }
 
-// M <= 32: the VALU kernel where it applies, else the MFMA streaming kernel (K split 4 ways per 16-row tile, 4 steps
-// of 128 bytes in flight per buffer; plain loads measured faster than non-temporal ones here).
+// M <= 32: the VALU kernel where it applies, else the LDS-ring MFMA streaming kernel.
 template <typename T, int EPI>
 static void launch_stream(const Args& p) {
     if (dot4_ok(p)) launch_dot4<T, EPI>(p);
-    else if (dot4l_pick(p)) launch_dot4l<T, EPI>(p);
-    else if (p.M <= 16) launch_stream_cfg<T, 1, 4, 4, 4, EPI, false>(p);
-    else launch_stream_cfg<T, 2, 4, 4, 4, EPI, false>(p);
+    else if (p.M <= 16) launch_stream_lds<T, 1, EPI>(p);
+    else launch_stream_lds<T, 2, EPI>(p);
 }
 
 // Main configuration: 256 x 256 tiles, 2 x 4 wavefronts of 128 x 64, 128-byte K stages, 2 in LDS (128 KB): measured
@@ -869,27 +769,23 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 }
 
 // Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
-// M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M <= 2 and K <= 17408 or
-// M = 3 and K <= 8192; kernel 3
-// = the prefill kernel's small configuration alone; kernel 4 = its main configuration alone; kernel 5 = the VALU
-// kernel with activations in LDS, 3 <= M <= 8, M * K <= 73728).  Returns -1 on bad arguments, else the launch error.
+// M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M = 1 and K <= 17408 or
+// M = 2 and K <= 8192; kernel 3 = the prefill kernel's small configuration alone; kernel 4 = its main configuration
+// alone).  Returns -1 on bad arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
-    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 5) return -1;
+    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 4) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
                  (hipStream_t)stream};
     if (kernel == 0) {
         if (M > 32) return -1;
-        if (M <= 16) launch_stream_cfg<f16, 1, 4, 4, 4, EPI_I32, false>(p);
-        else launch_stream_cfg<f16, 2, 4, 4, 4, EPI_I32, false>(p);
+        if (M <= 16) launch_stream_lds<f16, 1, EPI_I32>(p);
+        else launch_stream_lds<f16, 2, EPI_I32>(p);
     } else if (kernel == 1) {
         launch_gemm<f16, EPI_I32>(p);
     } else if (kernel == 3) {
         launch_gemm<f16, EPI_I32>(p, 2);
     } else if (kernel == 4) {
         launch_gemm<f16, EPI_I32>(p, 0);
-    } else if (kernel == 5) {
-        if (!dot4l_ok(p)) return -1;
-        launch_dot4l<f16, EPI_I32>(p);
     } else {
         if (!dot4_ok(p)) return -1;
         launch_dot4<f16, EPI_I32>(p);

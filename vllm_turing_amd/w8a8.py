@@ -5,8 +5,10 @@ vllm._custom_ops.cutlass_scaled_mm(a, b, scale_a, scale_b, out_dtype, bias); ins
 that runs the custom op vllm_turing_amd::scaled_mm_ (same arguments as vllm_turing::scaled_mm_, w8a8.py:104-122),
 which dispatches at run time on the concrete M (also under torch.compile and HIP graph capture, where the batch size
 is concrete):
-  * M <= VLLM_TURING_GEMV_MAX_M (default 12)           -> w8a8_gemv   (streaming int8 MFMA kernel, small-M epilogue)
-  * M <= VLLM_TURING_MMA_MAX_M (default and maximum 32) -> w8a8_mma    (same kernel, two 16-row activation tiles)
+  * M <= VLLM_TURING_GEMV_MAX_M (default 12)           -> w8a8_gemv   (weight-streaming kernels, small-M epilogue:
+    v_dot4 VALU kernel at one or two rows, else the LDS-ring int8 MFMA kernel)
+  * M <= VLLM_TURING_MMA_MAX_M (default and maximum 32) -> w8a8_mma    (the MFMA kernel, two 16-row activation tiles
+    past 16 rows)
   * M > MMA_MAX_M, no bias, per-row / per-column scales -> w8a8_big    (prefill MFMA GEMM, large-M epilogue)
   * anything else                                       -> w8a8_scaled_mm (prefill or streaming kernel with the
     large-M epilogue of vLLM's cutlass_scaled_mm, with bias / per-tensor scales; the reference sends these to vLLM's
