@@ -8,6 +8,7 @@ stream from HBM.  Launches are captured in a HIP graph of 20 back-to-back launch
 is GPU work only (HIP events on the launch stream, bracketed by synchronizations).
 
 Also reported:
+  decode_other_m: the same GEMV at M = 2, 4, 8;
   gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline);
   quant: per-token quant at M=4096, K=5120 and SiLU*up+quant at M=4096, I=17408, in GB/s (HBM-bound);
   cpu_baseline: the reference's CPU path restated (oracle/cpu_path.py: torch CPU int8 matmul + dequant), timed on a
@@ -321,6 +322,25 @@ def main():
     gemv_bytes = N * K + M * K + 2 * M * N + 4 * N + 4 * M
     gemv_gbs = gemv_bytes / (ms_gemv * 1e-3) / 1e9
     print(f"[bench] GEMV {ms_gemv * 1e3:.2f} us/launch, {gemv_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
+    # the other decode batch sizes of the same projection (M = 2, 4, 8), same weights and method
+    decode_m = {}
+    for Md in (2, 4, 8):
+        cd = workloads.decode(Md)
+        xq_d, xs_d = per_token_quant(cd["x"].to(dev))
+        out_d = torch.empty(Md, N, dtype=torch.float16, device=dev)
+
+        def gemv_d(i, Md=Md, xq_d=xq_d, xs_d=xs_d, out_d=out_d):
+            rc = L.w8a8_gemv(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(), None,
+                             out_d.data_ptr(), Md, N, K, 1, 1, 0, st())
+            if rc != 0:
+                raise RuntimeError(f"w8a8_gemv {rc}")
+
+        ms_d, _ = graph_time(torch, gemv_d, 4 * copies, 400, 40)
+        b_d = N * K + Md * K + 2 * Md * N + 4 * N + 4 * Md
+        decode_m[f"M{Md}"] = {"us": round(ms_d * 1e3, 2), "gbs": round(b_d / ms_d / 1e6, 1),
+                              "frac": round(b_d / ms_d / 1e6 / HBM_PEAK_GBS, 4)}
+    print(f"[bench] GEMV M=2/4/8: {decode_m}", file=sys.stderr, flush=True)
     del ws
 
     # ---- prefill GEMM, M=4096, bias, bf16 ---------------------------------------------------------------------------
@@ -408,6 +428,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_m1")},
         "cpu_baseline": cpu,
+        "decode_other_m": {"workload": f"decode W8A8 GEMV K={K} N={N}, fp16 out, same weights and method",
+                           **decode_m},
         "gemm": {"workload": f"prefill W8A8 GEMM M={Mg} K={Kg} N={Ng}, bias, bf16 out", "ms": round(ms_gemm, 4),
                  "launches": n_gemm, "tops": round(gemm_tops, 1),
                  "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS,
