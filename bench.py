@@ -272,34 +272,10 @@ def bench_stack(torch, L, st, dev, ms_list=(1, 4, 4096)):
     return res
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
-    ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--traffic", action="store_true", help="launch sequence for HBM-traffic counter runs")
-    ap.add_argument("--sections", default="headline,mlp,stack",
-                    help="comma list: headline (GEMV, GEMM, quant kernels; always run), mlp (MLP chain at M=4096), "
-                         "stack (64-layer sweep)")
-    args = ap.parse_args()
-    sections = set(args.sections.split(","))
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this W8A8 path has no multi-GPU mode (asked for --gpus {args.gpus})",
-              file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-    from vllm_turing_amd import _lib, workloads
+def bench_headline(torch, L, st, dev, args):
+    """Decode GEMV (M=1 headline, then M=2/4/8), prefill GEMM at M=4096, the quant kernels, the CPU baseline."""
+    from vllm_turing_amd import workloads
     from vllm_turing_amd.quantfuse import per_token_quant
-
-    dev = "cuda:0"
-    torch.cuda.set_device(0)
-    L = _lib.lib()
-    st = lambda: torch.cuda.current_stream().cuda_stream
-    if args.traffic:
-        traffic_sequence(torch, L, st, dev)
-        return
 
     # ---- decode GEMV, M=1 -----------------------------------------------------------------------------------------
     M, K, N = 1, workloads.HIDDEN, workloads.INTERMEDIATE
@@ -441,8 +417,42 @@ def main():
                   "silu_mul_quant_M4096_I17408": {"us": round(ms_s * 1e3, 2),
                                                    "gbs": round(smq_bytes / (ms_s * 1e-3) / 1e9, 1)}},
     }
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic", action="store_true", help="launch sequence for HBM-traffic counter runs")
+    ap.add_argument("--sections", default="headline,mlp,stack",
+                    help="comma list: headline (GEMV, GEMM, quant kernels, CPU baseline: the contract's JSON fields), "
+                         "mlp (MLP chain at M=4096), stack (64-layer sweep); profiling runs select one")
+    args = ap.parse_args()
+    sections = set(args.sections.split(","))
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this W8A8 path has no multi-GPU mode (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vllm_turing_amd import _lib
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    L = _lib.lib()
+    st = lambda: torch.cuda.current_stream().cuda_stream
+    if args.traffic:
+        traffic_sequence(torch, L, st, dev)
+        return
+
+    if "headline" in sections:
+        result = bench_headline(torch, L, st, dev, args)
+    else:
+        result = {"metric": METRIC, "sections": sorted(sections)}
     if "mlp" in sections:
-        del outg, wg, xq_in, qq, gu, qs
         torch.cuda.empty_cache()
         result["mlp_chain"] = bench_mlp(torch, L, st, dev)
     if "stack" in sections:
