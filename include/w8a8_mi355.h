@@ -57,6 +57,15 @@ int silu_mul_quant(const void* gu, void* q, void* scales, int M, int I, void* st
 /* The same for bfloat16 activations.  No counterpart in the reference (its kernel is fp16 only); same codes. */
 int silu_mul_quant_bf16(const void* gu, void* q, void* scales, int M, int I, void* stream);
 
+/* Residual add + RMSNorm + dynamic per-token int8 quantization: vLLM's rms_norm_dynamic_per_token_quant(input, weight,
+ * epsilon, torch.int8, scale_ub, residual), the producer of the gate_up input in the reference's MLP tail
+ * (vllm_turing/tailoverlap.py:145; the GemmaRMSNorm weight 1 + w is precomputed by the caller, :123).  x: [M, K]
+ * fp16 (dtype 0) or bf16 (dtype 1) row-major; residual: [M, K] of the same type, updated in place to RN(x + residual),
+ * or NULL; weight: [K]; scale_ub: one float32 bound on the row absmax, or NULL; q: [M, K] int8; scales: [M] float32.
+ * Returns 0, -1 on bad arguments, else the HIP launch error. */
+int rms_norm_quant(const void* x, void* residual, const void* weight, const void* scale_ub, float eps, void* q,
+                   void* scales, int M, int K, int dtype, void* stream);
+
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
  * checks: kernel 0 the small-M MFMA streaming kernel (M <= 32), 1 the prefill kernel as dispatched, 2 the v_dot4
  * streaming kernel (M = 1 and K <= 17408, or M = 2 and K <= 8192), 3 and 4 the prefill kernel's quarter-tile and

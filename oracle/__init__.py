@@ -41,6 +41,7 @@ def lib():
         L.o_silu_h.restype = ctypes.c_uint16
         L.o_silu_table.argtypes = [i, vp]
         L.o_silu_mul_quant.argtypes = [vp, i, lg, lg, vp, vp, vp]
+        L.o_rms_norm_quant.argtypes = [vp, vp, vp, vp, ctypes.c_float, lg, lg, i, vp, vp, vp, vp]
         L.o_h2f.argtypes = [ctypes.c_uint16]
         L.o_h2f.restype = ctypes.c_float
         L.o_f2h.argtypes = [ctypes.c_float]
@@ -132,6 +133,34 @@ def silu_mul_quant(gu):
     act = np.empty((M, I), np.uint16)
     lib().o_silu_mul_quant(_p(gb), code, M, I, _p(q), _p(s), _p(act))
     return q, s, act
+
+
+def rms_norm_quant(x, weight, eps, residual=None, scale_ub=None):
+    """Residual add + RMSNorm + per-token int8 quant (vLLM's rms_norm_dynamic_per_token_quant as the reference calls it,
+    vllm_turing/tailoverlap.py:145; the contract of o_rms_norm_quant).
+
+    x, residual: [M, K] fp16/bf16; weight: [K] of the same type; eps: float; scale_ub: float or None.
+    Returns (q int8 [M, K], scales float32 [M], new residual bit patterns uint16 [M, K] or None,
+    normalised row bit patterns uint16 [M, K])."""
+    xb, code = _bits(x)
+    wb, wcode = _bits(weight)
+    if wcode != code:
+        raise TypeError("weight dtype differs from the input's")
+    M, K = xb.shape
+    rb = None
+    if residual is not None:
+        rb, rcode = _bits(residual)
+        if rcode != code:
+            raise TypeError("residual dtype differs from the input's")
+        rb = rb.copy()
+    q = np.empty((M, K), np.int8)
+    s = np.empty(M, np.float32)
+    y = np.empty((M, K), np.uint16)
+    sbuf = np.empty(K, np.float32)
+    ubv = None if scale_ub is None else np.array([scale_ub], np.float32)
+    lib().o_rms_norm_quant(_p(xb), None if rb is None else _p(rb), _p(np.ascontiguousarray(wb.reshape(-1))),
+                           None if ubv is None else _p(ubv), float(eps), M, K, code, _p(q), _p(s), _p(y), _p(sbuf))
+    return q, s, rb, y
 
 
 def scaled_mm(a_q, w_q, sa, sw, bias=None, dtype=FP16, order=None):

@@ -18,9 +18,15 @@
  *                       60 digits and correctly rounded to float32 (the reference's CUDA expf itself cannot be run or
  *                       reproduced; rare 1-ulp differences of CUDA's expf are the one unpinned residue).
  *   o_silu_mul_quant    pinned: composition of the above; the fp16 product is exact IEEE.
+ *   o_rms_norm_quant    pinned: residual sum against numpy / torch IEEE conversion, the normalised row against the
+ *                       float64 closed form within one 16-bit rounding, rms within 1.5 float32 ulps of the float64
+ *                       value, known answers (constant rows -> +-127, zero row -> scale FLT_EPSILON and q = 0) and the
+ *                       quant invariants.  Bit-level parity with vLLM's own op (third-party, absent; float32 block
+ *                       sum and rsqrtf) is unpinned, see the function.
  *
  * Build: oracle/Makefile (gcc -O3 -ffp-contract=off -fno-fast-math; SSE2 float arithmetic on x86-64).
  */
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
@@ -208,5 +214,60 @@ void o_silu_mul_quant(const uint16_t* gu, int dtype, long M, long I, int8_t* q, 
         const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
         s[m] = amax / 127.0f;
         for (long i = 0; i < I; ++i) q[m * I + i] = q8(to_f(r[i], dtype) * inv);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * Fused residual add + RMSNorm + dynamic per-token int8 quantization: the producer of the gate_up input in the
+ * reference's MLP tail, ops.rms_norm_dynamic_per_token_quant(h, w1, eps, torch.int8, None, res) at
+ * vllm_turing/tailoverlap.py:145 (w1 = 1 + w precomputed for GemmaRMSNorm at :123).  The op is vLLM's (third-party,
+ * not in the reference tree); restated from its published kernel, per row:
+ *   s[k]  = float(x[k]) + float(r[k])                       (r absent: s = float(x))
+ *   r[k]  = RN_T(s[k])                                      (the residual is updated in place)
+ *   rms   = 1 / sqrt(mean(s^2) + eps)
+ *   y[k]  = float( RN_T( float(RN_T(RN32(s[k] * rms))) * float(w[k]) ) )   (the 16-bit product is exact in float)
+ *   scale = max(RN32(min(absmax(y), ub) / 127), FLT_EPSILON);  q[k] = clamp(rint(RN32(y[k] * RN32(1 / scale))))
+ * vLLM sums s^2 in float32 in its block-reduction order and takes rsqrtf; this build's contract fixes both: the sum
+ * is taken in float64 (each square exact, the sum order-free to ~1e-12) and rounded once, ms = RN32(ss / K), and
+ * rms = RN32(1 / RN32(sqrt(RN32(ms + eps)))).  The unpinned residue against vLLM is therefore the last float32 bit of
+ * rms, which moves a 16-bit y only when s * rms sits within ~1e-6 of a rounding boundary.
+ * x: [M, K] bit patterns (row stride K); res: [M, K] or NULL, updated; w: [K]; ub: scale upper bound or NULL;
+ * q: [M, K]; s: [M]; y (optional, may be NULL): the normalised 16-bit row, [M, K].
+ * ------------------------------------------------------------------------------------------------------------------ */
+void o_rms_norm_quant(const uint16_t* x, uint16_t* res, const uint16_t* w, const float* ub, float eps, long M, long K,
+                      int dtype, int8_t* q, float* scales, uint16_t* y, float* sbuf) {
+    /* sbuf: caller scratch of K floats (the row's s) */
+    for (long m = 0; m < M; ++m) {
+        const uint16_t* xr = x + m * K;
+        uint16_t* rr = res ? res + m * K : 0;
+        double ss = 0.0;
+        for (long k = 0; k < K; ++k) {
+            float v = to_f(xr[k], dtype);
+            if (rr) {
+                v = v + to_f(rr[k], dtype);
+                rr[k] = from_f(v, dtype);
+            }
+            sbuf[k] = v;
+            ss += (double)v * (double)v;                         /* exact square of a float in double */
+        }
+        const float ms = (float)(ss / (double)K);
+        const float rms = 1.0f / sqrtf(ms + eps);
+        float amax = 0.0f;
+        for (long k = 0; k < K; ++k) {
+            const float t = sbuf[k] * rms;
+            const float p = to_f(from_f(t, dtype), dtype) * to_f(w[k], dtype);    /* exact */
+            const uint16_t yb = from_f(p, dtype);
+            if (y) y[m * K + k] = yb;
+            const float yv = to_f(yb, dtype);
+            sbuf[k] = yv;
+            if (fabsf(yv) > amax) amax = fabsf(yv);
+        }
+        float a = amax;
+        if (ub && *ub < a) a = *ub;
+        float scale = a / 127.0f;
+        if (!(scale >= FLT_EPSILON)) scale = FLT_EPSILON;
+        scales[m] = scale;
+        const float inv = 1.0f / scale;
+        for (long k = 0; k < K; ++k) q[m * K + k] = q8(sbuf[k] * inv);
     }
 }

@@ -94,6 +94,71 @@ def test_device_rounding(L, dt):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# residual add + RMSNorm + per-token quant
+# ---------------------------------------------------------------------------------------------------------------------
+RNQ_CASES = [(1, 5120), (7, 5120), (300, 5120), (4, 17408), (3, 6144), (2, 136), (5, 8), (3, 5001), (2, 65536),
+             (16, 49152)]
+
+
+@pytest.mark.parametrize("with_res", [True, False])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K", RNQ_CASES)
+def test_rms_norm_quant(L, dt, M, K, with_res):
+    say(f"rms_norm_quant M={M} K={K} {dt} residual={with_res}")
+    g = torch.Generator().manual_seed(M * 13 + K)
+    x = (torch.randn(M, K, generator=g) * 3).to(dt)
+    if K >= 64:
+        x[:, ::61] *= 25                                   # outlier channels
+    if M > 2:
+        x[1] = 0                                           # a zero input row (with a residual: the residual's norm)
+    r = torch.randn(M, K, generator=g).to(dt) if with_res else None
+    if with_res and M > 2:
+        r[1] = 0                                           # zero row: scale FLT_EPSILON, q = 0
+    w = (torch.rand(K, generator=g) * 1.5 + 0.25).to(dt)
+    xd, wd = x.to(DEV), w.to(DEV)
+    rd = r.to(DEV) if with_res else None
+    q = torch.empty(M, K, dtype=torch.int8, device=DEV)
+    s = torch.empty(M, dtype=torch.float32, device=DEV)
+    rc = L.rms_norm_quant(xd.data_ptr(), rd.data_ptr() if with_res else None, wd.data_ptr(), None, 1e-6, q.data_ptr(),
+                          s.data_ptr(), M, K, code(dt), stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    qr, sr, rr, _ = oracle.rms_norm_quant(x, w, 1e-6, r)
+    assert np.array_equal(q.cpu().numpy(), qr), f"{int((q.cpu().numpy() != qr).sum())} int8 differ"
+    assert np.array_equal(s.cpu().numpy(), sr)
+    if with_res:
+        assert np.array_equal(bits(rd), rr)
+
+
+def test_rms_norm_quant_api(L):
+    """vLLM's signature: residual updated in place, scale_ub, [rows, 1] scales, leading dims kept."""
+    say("rms_norm_dynamic_per_token_quant api")
+    from vllm_turing_amd import rms_norm_dynamic_per_token_quant
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(2, 3, 5120, generator=g).to(torch.bfloat16)
+    res = torch.randn(2, 3, 5120, generator=g).to(torch.bfloat16)
+    w = (torch.rand(5120, generator=g) + 0.5).to(torch.bfloat16)
+    res_d = res.to(DEV)
+    ub = torch.tensor([2.0])
+    q, s = rms_norm_dynamic_per_token_quant(h.to(DEV), w.to(DEV), 1e-6, torch.int8, ub.to(DEV), res_d)
+    torch.cuda.synchronize()
+    assert q.shape == (2, 3, 5120) and s.shape == (6, 1)
+    qr, sr, rr, _ = oracle.rms_norm_quant(h.reshape(6, 5120), w, 1e-6, res.reshape(6, 5120), scale_ub=2.0)
+    assert np.array_equal(q.reshape(6, 5120).cpu().numpy(), qr)
+    assert np.array_equal(s.view(-1).cpu().numpy(), sr)
+    assert np.array_equal(bits(res_d).reshape(6, 5120), rr)
+    with pytest.raises(NotImplementedError):
+        rms_norm_dynamic_per_token_quant(h.to(DEV), w.to(DEV), 1e-6, torch.float8_e4m3fn)
+
+
+def test_rms_norm_quant_codes(L):
+    assert L.rms_norm_quant(None, None, None, None, 1e-6, None, None, 4, 64, 0, None) == -1
+    assert L.rms_norm_quant(16, None, 16, None, 1e-6, 16, 16, 4, 64, 2, None) == -1
+    assert L.rms_norm_quant(16, None, 16, None, -1.0, 16, 16, 4, 64, 0, None) == -1
+    assert L.rms_norm_quant(16, None, 16, None, 1e-6, 16, 16, 0, 64, 0, None) == 0
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # per-token quant
 # ---------------------------------------------------------------------------------------------------------------------
 QUANT_CASES = [(1, 5120), (5, 5120), (16, 5120), (300, 5120), (7, 17408), (3, 136), (4, 8), (2, 131072), (9, 5001), (3, 7),
@@ -365,6 +430,31 @@ def test_prefill_config_sampled(L, M):
                           stream()) == 0
     torch.cuda.synchronize()
     assert torch.equal(acc1 + acc2, acc)
+
+
+def test_mlp_tail_fused(L):
+    """tailoverlap.py:145-151's fused tail: residual add + RMSNorm + quant -> gate_up -> SiLU*up+quant -> down, every
+    intermediate bit-exact (M = 64, the C4 widths, GemmaRMSNorm weight 1 + w)."""
+    say("mlp tail fused")
+    from vllm_turing_amd import workloads, mlp_tail
+    from vllm_turing_amd.normquant import gemma_weight
+    c = workloads.mlp(M=64)
+    g = torch.Generator().manual_seed(9)
+    h = c["x"]
+    res = (torch.randn(64, workloads.HIDDEN, generator=g) * 0.5).to(torch.bfloat16)
+    w1 = gemma_weight((torch.randn(workloads.HIDDEN, generator=g) * 0.1).to(torch.bfloat16))
+    res_d = res.to(DEV)
+    wgu, wd = c["w_gate_up"].to(DEV), c["w_down"].to(DEV)
+    out = mlp_tail(h.to(DEV), res_d, w1.to(DEV), 1e-6, wgu, c["sw_gate_up"].to(DEV), wd, c["sw_down"].to(DEV))
+    torch.cuda.synchronize()
+    qr, sr, rr, _ = oracle.rms_norm_quant(h, w1, 1e-6, res)
+    assert np.array_equal(bits(res_d), rr)
+    gu_ref, _ = cpu_path.scaled_mm(torch.from_numpy(qr), c["w_gate_up"], torch.from_numpy(sr), c["sw_gate_up"], None,
+                                   torch.bfloat16, 1)
+    aq_r, as_r, _ = oracle.silu_mul_quant(gu_ref)
+    o_ref, _ = cpu_path.scaled_mm(torch.from_numpy(aq_r), c["w_down"], torch.from_numpy(as_r), c["sw_down"], None,
+                                  torch.bfloat16, 1)
+    assert torch.equal(out.cpu(), o_ref)
 
 
 def test_mlp_chain_small(L):

@@ -9,7 +9,9 @@ int32 -> float conversion, a missed zero-row rule) fails it:
   * int32 GEMM: torch._int_mm (oneDNN VNNI) and a float64 matmul, brute force on tiny shapes;
   * epilogues: exact rational arithmetic (fractions.Fraction) with correct rounding at each step the reference
     rounds, plus the float64 closed form of the reference's own test (tests/test_w8a8_mma.py:43-51);
-  * per-token quant: hand-computed known answers, invariants, and a case where x / scale differs from x * inverse.
+  * per-token quant: hand-computed known answers, invariants, and a case where x / scale differs from x * inverse;
+  * residual add + RMSNorm + quant: the residual against torch's IEEE float32 add and RN conversion, the normalised
+    row against the float64 closed form within one 16-bit ulp, constant and zero rows, the scale bound, invariants.
 """
 import decimal
 import math
@@ -344,3 +346,89 @@ def test_silu_mul_quant_composition(oracle_lib):
         q2, s2 = oracle_lib.quant_rows(ref_act)
         assert np.array_equal(q, q2) and np.array_equal(s, s2)
         assert np.all(q[0] == 0) and s[0] == 0
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# residual add + RMSNorm + per-token quant (vLLM's rms_norm_dynamic_per_token_quant as tailoverlap.py:145 calls it)
+# ---------------------------------------------------------------------------------------------------------------------
+def _ulp16(v, dt):
+    """Spacing of the 16-bit format at |v| (float64 array)."""
+    mant, emin = (10, -14) if dt == torch.float16 else (7, -126)
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** emin)))
+    return 2.0 ** (e - mant)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("with_res", [True, False])
+def test_rms_norm_quant_closed_form(oracle_lib, dt, with_res):
+    g = torch.Generator().manual_seed(11)
+    M, K, eps = 6, 5120, 1e-6
+    x = (torch.randn(M, K, generator=g) * 2).to(dt)
+    x[1, ::97] *= 40                                       # outlier channels
+    r = torch.randn(M, K, generator=g).to(dt) if with_res else None
+    w = (torch.rand(K, generator=g) + 0.5).to(dt)
+    q, s, rb, y = oracle.rms_norm_quant(x, w, eps, r)
+    sf = x.float() + (r.float() if with_res else 0)        # torch IEEE float32 add
+    if with_res:
+        want = sf.to(dt).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(rb, want)
+    s64 = sf.double()
+    rms64 = 1.0 / torch.sqrt((s64 * s64).mean(dim=1, keepdim=True) + eps)
+    t64 = (s64 * rms64).numpy()
+    y64 = (s64 * rms64 * w.double()).numpy()
+    yv = torch.from_numpy(y.view(np.int16)).view(dt).double().numpy()
+    # two 16-bit roundings (of s * rms, then of the product with w): |error| <= ulp(t) w / 2 + ulp(y) / 2
+    bound = 0.5 * _ulp16(t64, dt) * w.double().numpy() + 0.5 * _ulp16(y64, dt)
+    assert np.all(np.abs(yv - y64) <= bound * (1 + 1e-5))
+    # the documented chain with numpy float32 arithmetic and torch's conversions (a second implementation of the
+    # contract: a dropped intermediate rounding or a fused product fails here)
+    ms = np.float32((sf.double() ** 2).sum(dim=1).numpy() / K)
+    rms32 = np.float32(1) / np.sqrt(ms + np.float32(eps))
+    t32 = torch.from_numpy(sf.numpy() * rms32[:, None]).to(dt).float()
+    y32 = (t32 * w.float()).to(dt)
+    assert np.array_equal(y, y32.view(torch.int16).numpy().view(np.uint16))
+    # quant: scale = absmax / 127 in float32, q = rint(y * RN32(1 / scale)) saturated, +-127 at the argmax
+    absmax = np.abs(yv).max(axis=1).astype(np.float32)
+    assert np.array_equal(s, np.maximum(absmax / np.float32(127), np.float32(np.finfo(np.float32).eps)))
+    inv = np.float32(1) / s
+    ref_q = np.clip(np.rint(yv.astype(np.float32) * inv[:, None]), -128, 127).astype(np.int8)
+    assert np.array_equal(q, ref_q)
+    assert np.abs(q.astype(int)).max() <= 127
+    am = np.abs(yv).argmax(axis=1)
+    assert np.all(np.abs(q[np.arange(M), am].astype(int)) == 127)
+
+
+def test_rms_norm_quant_known_rows(oracle_lib):
+    K = 4096
+    for dt in (torch.float16, torch.bfloat16):
+        x = torch.zeros(3, K, dtype=dt)
+        x[0] = 0.75                                        # constant row: y = +1 everywhere -> q = 127, scale 1/127
+        x[1] = -3.0                                        # constant negative row, weight 1: q = -127
+        w = torch.ones(K, dtype=dt)
+        q, s, rb, y = oracle.rms_norm_quant(x, w, 1e-6)
+        assert rb is None
+        assert np.all(q[0] == 127) and np.all(q[1] == -127)
+        assert s[0] == np.float32(1) / np.float32(127) and s[1] == s[0]
+        assert np.all(q[2] == 0) and s[2] == np.finfo(np.float32).eps    # zero row: the minimum scale, q = 0
+        # residual that cancels the input: s = 0 -> zero output, residual becomes +0 / -0 sums
+        r = -x
+        q2, s2, rb2, _ = oracle.rms_norm_quant(x, w, 1e-6, r)
+        assert np.all(q2 == 0) and np.all(s2 == np.finfo(np.float32).eps)
+        assert np.all(torch.from_numpy(rb2.view(np.int16)).view(dt).float().numpy() == 0)
+
+
+def test_rms_norm_quant_scale_bound(oracle_lib):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(4, 1024, generator=g).half()
+    w = torch.ones(1024).half()
+    q, s, _, y = oracle.rms_norm_quant(x, w, 1e-5)
+    ub = float(s.min()) * 127 / 2                           # below every row's absmax
+    q2, s2, _, y2 = oracle.rms_norm_quant(x, w, 1e-5, scale_ub=ub)
+    assert np.array_equal(y, y2)
+    assert np.all(s2 == np.float32(np.float32(ub) / np.float32(127)))
+    # a scale below the row's absmax saturates the largest values at -128 / 127 (vLLM's float_to_int8_rn clamp)
+    assert q2.min() >= -128 and q2.max() <= 127
+    assert ((q2 == 127) | (q2 == -128)).sum() > ((q == 127) | (q == -128)).sum()
+    inv = np.float32(1) / s2
+    yv = torch.from_numpy(y2.view(np.int16)).view(torch.float16).float().numpy()
+    assert np.array_equal(q2, np.clip(np.rint(yv * inv[:, None]), -128, 127).astype(np.int8))

@@ -5,7 +5,8 @@ int8 MFMA GEMV for decode and an LDS-tiled int8 MFMA GEMM for prefill, each with
 C ABI (include/w8a8_mi355.h) loaded with ctypes, and Python hooks with the reference plugin's signatures:
   w8a8.cutlass_scaled_mm / torch.ops.vllm_turing_amd.scaled_mm_   (vllm_turing/w8a8.py)
   quantfuse.scaled_int8_quant / quant_torch                         (vllm_turing/quantfuse.py)
-  tailoverlap.silu_mul_quant                                        (vllm_turing/tailoverlap.py)
+  tailoverlap.silu_mul_quant / mlp_tail                             (vllm_turing/tailoverlap.py)
+  normquant.rms_norm_dynamic_per_token_quant                        (vLLM's fused op, tailoverlap.py:145)
 register() mirrors the reference plugin entry point (vllm_turing/__init__.py:38-72): with vLLM importable on a gfx950
 device it patches vllm._custom_ops; VLLM_TURING_DISABLE=1 turns it off.  Importing the package builds nothing; the
 library is built or loaded on first use.
@@ -16,10 +17,11 @@ import os
 logger = logging.getLogger("vllm.turing_amd")
 _registered = False
 
-from . import quantfuse, w8a8  # noqa: E402  (defines the custom ops)
+from . import normquant, quantfuse, w8a8  # noqa: E402  (defines the custom ops)
 from .linear import W8A8Linear, W8A8LinearMethod  # noqa: E402,F401
+from .normquant import rms_norm_dynamic_per_token_quant  # noqa: E402,F401
 from .quantfuse import per_token_quant, quant_torch, scaled_int8_quant  # noqa: E402,F401
-from .tailoverlap import mlp, mlp_quantized, silu_mul_quant  # noqa: E402,F401
+from .tailoverlap import mlp, mlp_quantized, mlp_tail, silu_mul_quant  # noqa: E402,F401
 from .w8a8 import cutlass_scaled_mm  # noqa: E402,F401
 
 
@@ -30,6 +32,8 @@ def register():
         return
     _registered = True
     q = quantfuse.install()
+    n = normquant.install()
     m = w8a8.install()
-    logger.info("vllm_turing_amd: scaled_int8_quant hook %s, cutlass_scaled_mm hook %s (GEMV up to M=%d)",
-                "on" if q else "off", "on" if m else "off", w8a8.MAX_M)
+    logger.info("vllm_turing_amd: scaled_int8_quant hook %s, rms_norm_dynamic_per_token_quant hook %s, "
+                "cutlass_scaled_mm hook %s (GEMV up to M=%d)", "on" if q else "off", "on" if n else "off",
+                "on" if m else "off", w8a8.MAX_M)

@@ -14,6 +14,13 @@
 // silu depends only on the 16-bit input, so it is checked exhaustively: on all 65,536 fp16 and all 65,536 bf16 inputs
 // the float32 result of this expression is within 2 float32 ulps of the one built on a correctly rounded exp and
 // rounds to the same 16-bit value (GPU test against the oracle's table).
+//
+// A third kernel fuses the residual add and the RMSNorm in front of the quantization (vLLM's
+// rms_norm_dynamic_per_token_quant as vllm_turing/tailoverlap.py:145 calls it): s = x + r (float), r <- RN_T(s),
+// rms = 1 / sqrt(RN32(sum s^2 / K) + eps) with the sum of squares in float64 (each square exact, the sum order-free to
+// ~1e-12), y = RN_T(float(RN_T(s * rms)) * w), scale = max(absmax(y) / 127, FLT_EPSILON), q = rint(y * (1 / scale)).
+#include <float.h>
+
 #include "common.h"
 #include "../../include/w8a8_mi355.h"
 
@@ -159,6 +166,160 @@ __global__ void silu_table_kernel(uint16_t* __restrict__ out) {
     if (i < 65536) out[i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
 }
 
+// ---- residual add + RMSNorm + per-token quant ----------------------------------------------------------------------
+constexpr int MAX_VPT_NORM = 6;                          // input + residual in registers: 8 VGPRs a vector
+
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);   // butterfly: every lane holds the sum
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    double t = red[0];
+    for (int i = 1; i < nw; ++i) t += red[i];                            // fixed order: identical in every thread
+    return t;
+}
+
+// One block per row, the row (input and residual) in registers.  RES: a residual is added and updated in place.
+template <typename T, int VPT, bool RES>
+__global__ void __launch_bounds__(1024) rms_norm_quant_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
+                                                              const uint16_t* __restrict__ w,
+                                                              const float* __restrict__ ub, float eps,
+                                                              int8_t* __restrict__ q, float* __restrict__ scales,
+                                                              int K) {
+    __shared__ double redd[16];
+    __shared__ float red[16];
+    const long row = blockIdx.x;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * (long)K);
+    uint4* rr = reinterpret_cast<uint4*>(res + row * (long)K);          // used only with RES
+    const uint4* w4 = reinterpret_cast<const uint4*>(w);
+    const int nvec = K >> 3;
+    uint4 xv[VPT], rv[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        xv[j] = idx < nvec ? xr[idx] : make_uint4(0, 0, 0, 0);
+        rv[j] = RES && idx < nvec ? rr[idx] : make_uint4(0, 0, 0, 0);
+    }
+    auto sum_at = [&](int j, int e, bool hi) -> float {                  // s = float(x) + float(r), one rounding
+        const uint32_t xw = e == 0 ? xv[j].x : e == 1 ? xv[j].y : e == 2 ? xv[j].z : xv[j].w;
+        const float xf = hi ? hi_half(xw, T{}) : lo_half(xw, T{});
+        if constexpr (!RES) return xf;
+        const uint32_t rw = e == 0 ? rv[j].x : e == 1 ? rv[j].y : e == 2 ? rv[j].z : rv[j].w;
+        return xf + (hi ? hi_half(rw, T{}) : lo_half(rw, T{}));
+    };
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        if (idx < nvec) {
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = sum_at(j, e, false), hi = sum_at(j, e, true);
+                ss += (double)lo * (double)lo;
+                ss += (double)hi * (double)hi;
+                o[e] = (uint32_t)from_float<T>(lo) | ((uint32_t)from_float<T>(hi) << 16);
+            }
+            if constexpr (RES) rr[idx] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+    ss = block_sum_d(ss, redd);
+    const float ms = (float)(ss / (double)K);
+    const float rms = 1.0f / sqrtf(ms + eps);                            // IEEE sqrt and division
+
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        uint32_t o[4] = {0, 0, 0, 0};
+        if (idx < nvec) {
+            const uint4 wv = w4[idx];
+            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint16_t yb[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float t = sum_at(j, e, h == 1) * rms;
+                    const float n = to_float(T{from_float<T>(t)});
+                    const float p = n * (h ? hi_half(ww[e], T{}) : lo_half(ww[e], T{}));   // exact product
+                    yb[h] = from_float<T>(p);
+                    amax = __builtin_fmaxf(amax, __builtin_fabsf(to_float(T{yb[h]})));
+                }
+                o[e] = (uint32_t)yb[0] | ((uint32_t)yb[1] << 16);
+            }
+        }
+        xv[j] = make_uint4(o[0], o[1], o[2], o[3]);                    // y replaces x
+    }
+    amax = block_max(amax, red);
+    const float a = ub && *ub < amax ? *ub : amax;
+    float scale = a / 127.0f;
+    if (!(scale >= FLT_EPSILON)) scale = FLT_EPSILON;
+    const float inv = 1.0f / scale;
+    if (threadIdx.x == 0) scales[row] = scale;
+    uint2* qo = reinterpret_cast<uint2*>(q + row * (long)K);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int idx = threadIdx.x + j * blockDim.x;
+        if (idx < nvec) {
+            const uint32_t yw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            int b[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b[2 * e] = q8(lo_half(yw[e], T{}) * inv);
+                b[2 * e + 1] = q8(hi_half(yw[e], T{}) * inv);
+            }
+            qo[idx] = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
+        }
+    }
+}
+
+// Any K and alignment: three passes over the row (input and residual re-read from L2), the residual written last.
+template <typename T>
+__global__ void __launch_bounds__(256) rms_norm_quant_any_kernel(const uint16_t* __restrict__ x,
+                                                                 uint16_t* __restrict__ res,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 const float* __restrict__ ub, float eps,
+                                                                 int8_t* __restrict__ q, float* __restrict__ scales,
+                                                                 int K) {
+    __shared__ double redd[16];
+    __shared__ float red[16];
+    const long row = blockIdx.x;
+    const uint16_t* xr = x + row * (long)K;
+    uint16_t* rr = res ? res + row * (long)K : nullptr;
+    auto sum_at = [&](int k) -> float {
+        const float xf = to_float(T{xr[k]});
+        return rr ? xf + to_float(T{rr[k]}) : xf;
+    };
+    double ss = 0.0;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const float v = sum_at(k);
+        ss += (double)v * (double)v;
+    }
+    ss = block_sum_d(ss, redd);
+    const float ms = (float)(ss / (double)K);
+    const float rms = 1.0f / sqrtf(ms + eps);
+    auto y_at = [&](int k) -> float {
+        const float n = to_float(T{from_float<T>(sum_at(k) * rms)});
+        return to_float(T{from_float<T>(n * to_float(T{w[k]}))});
+    };
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) amax = __builtin_fmaxf(amax, __builtin_fabsf(y_at(k)));
+    amax = block_max(amax, red);
+    const float a = ub && *ub < amax ? *ub : amax;
+    float scale = a / 127.0f;
+    if (!(scale >= FLT_EPSILON)) scale = FLT_EPSILON;
+    const float inv = 1.0f / scale;
+    if (threadIdx.x == 0) scales[row] = scale;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        q[row * (long)K + k] = (int8_t)q8(y_at(k) * inv);
+        if (rr) rr[k] = from_float<T>(sum_at(k));       // after every read of this element's residual
+    }
+}
+
 // float32 -> 16-bit rounding of the epilogues and the SiLU kernel (test export).
 template <typename T>
 __global__ void round16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out, long n) {
@@ -220,6 +381,40 @@ static int run_smq(const void* gu, void* q, void* s, int M, int I, hipStream_t s
     return 0;
 }
 
+template <typename T, bool RES>
+static int run_rnq_res(const void* x, void* res, const void* w, const float* ub, float eps, void* q, void* s, int M,
+                       int K, hipStream_t st) {
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    uint16_t* rp = static_cast<uint16_t*>(res);
+    const uint16_t* wp = static_cast<const uint16_t*>(w);
+    int8_t* qp = static_cast<int8_t*>(q);
+    float* sp = static_cast<float*>(s);
+    int vpt = 0;
+    const int threads = pick_threads(K / 8, MAX_VPT_NORM, &vpt);
+    switch (vpt) {
+#define W8_CASE(V) case V: rms_norm_quant_kernel<T, V, RES><<<M, threads, 0, st>>>(xp, rp, wp, ub, eps, qp, sp, K); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6)
+#undef W8_CASE
+        default: return -1;
+    }
+    return 0;
+}
+
+template <typename T>
+static int run_rnq(const void* x, void* res, const void* w, const float* ub, float eps, void* q, void* s, int M, int K,
+                   hipStream_t st) {
+    const bool vec_ok = K % 8 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)res % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+                        (uintptr_t)q % 8 == 0 && (K / 8 + 1023) / 1024 <= MAX_VPT_NORM;
+    if (!vec_ok) {
+        rms_norm_quant_any_kernel<T><<<M, 256, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(res),
+                                                         static_cast<const uint16_t*>(w), ub, eps,
+                                                         static_cast<int8_t*>(q), static_cast<float*>(s), K);
+        return 0;
+    }
+    return res ? run_rnq_res<T, true>(x, res, w, ub, eps, q, s, M, K, st)
+               : run_rnq_res<T, false>(x, res, w, ub, eps, q, s, M, K, st);
+}
+
 }  // namespace w8
 
 using namespace w8;
@@ -276,5 +471,23 @@ extern "C" int f32_to_16(const void* x, void* out, long n, int dtype, void* stre
     const long blocks = (n + 255) / 256;
     if (dtype == DT_F16) round16_kernel<f16><<<blocks, 256, 0, st>>>(static_cast<const float*>(x), static_cast<uint16_t*>(out), n);
     else round16_kernel<bf16><<<blocks, 256, 0, st>>>(static_cast<const float*>(x), static_cast<uint16_t*>(out), n);
+    return (int)hipGetLastError();
+}
+
+// Residual add + RMSNorm + dynamic per-token int8 quantization: vLLM's rms_norm_dynamic_per_token_quant(input, weight,
+// epsilon, int8, scale_ub, residual) as the reference's MLP tail calls it (vllm_turing/tailoverlap.py:145).
+// x: [M, K] fp16 (dtype 0) or bf16 (dtype 1), row-major; residual: [M, K] of the same type, updated in place to
+// RN(x + residual), or null; weight: [K]; scale_ub: one float32 upper bound on the row absmax, or null; q: [M, K]
+// int8; scales: [M] float32.  Returns 0, -1 on bad arguments, or the HIP launch error.
+extern "C" int rms_norm_quant(const void* x, void* residual, const void* weight, const void* scale_ub, float eps,
+                              void* q, void* scales, int M, int K, int dtype, void* stream) {
+    if (M < 0 || K < 1 || (dtype != DT_F16 && dtype != DT_BF16) || !x || !weight || !q || !scales || !(eps >= 0.0f))
+        return -1;
+    if (M == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const float* ub = static_cast<const float*>(scale_ub);
+    const int rc = dtype == DT_F16 ? run_rnq<f16>(x, residual, weight, ub, eps, q, scales, M, K, st)
+                                   : run_rnq<bf16>(x, residual, weight, ub, eps, q, scales, M, K, st);
+    if (rc != 0) return rc;
     return (int)hipGetLastError();
 }

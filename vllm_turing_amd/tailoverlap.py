@@ -2,12 +2,14 @@
 and the MLP chain that uses it, on MI355X HIP kernels.
 
 The counterpart of the in-scope part of vllm_turing/tailoverlap.py: silu_mul_quant(gate_up) (:57-66) and the
-quantized MLP of _Tail.mlp_partial (:138-157): gate_up W8A8 GEMM -> SiLU * up + int8 requant -> down W8A8 GEMM.  The
-token chunking, side streams and all-reduce overlap of that module are multi-GPU and not part of this path.
+quantized MLP of _Tail.mlp_partial (:138-157): residual add + RMSNorm + int8 quant -> gate_up W8A8 GEMM -> SiLU * up +
+int8 requant -> down W8A8 GEMM.  The token chunking, side streams and all-reduce overlap of that module are multi-GPU
+and not part of this path.
 """
 import torch
 
 from . import _lib
+from .normquant import rms_norm_dynamic_per_token_quant
 from .quantfuse import per_token_quant
 from .w8a8 import cutlass_scaled_mm
 
@@ -59,3 +61,11 @@ def mlp(x, w_gate_up, sw_gate_up, w_down, sw_down):
     """The same chain from a floating-point input (per-token quantization of x first)."""
     x_q, x_s = per_token_quant(x)
     return mlp_quantized(x_q, x_s, w_gate_up, sw_gate_up, w_down, sw_down, x.dtype)
+
+
+def mlp_tail(h, residual, norm_weight, eps, w_gate_up, sw_gate_up, w_down, sw_down):
+    """_Tail.mlp_partial's fused path (tailoverlap.py:138-151): residual += h in place, x_q = int8 RMSNorm(residual)
+    (norm_weight as the fused op takes it: 1 + w for GemmaRMSNorm), then the quantized MLP; returns the down
+    projection in h's dtype."""
+    x_q, x_s = rms_norm_dynamic_per_token_quant(h, norm_weight, eps, torch.int8, None, residual)
+    return mlp_quantized(x_q, x_s, w_gate_up, sw_gate_up, w_down, sw_down, h.dtype)
