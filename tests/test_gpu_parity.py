@@ -457,6 +457,33 @@ def test_mlp_tail_fused(L):
     assert torch.equal(out.cpu(), o_ref)
 
 
+def test_checkpoint_layers_forward(L, tmp_path):
+    """A converted compressed-tensors W8A8 checkpoint loaded onto the GPU: each layer's forward (per-token quant +
+    scaled int8 matmul through the dispatch) bit-exact against the oracle, at decode and prefill row counts."""
+    say("checkpoint layers forward")
+    import sys
+    sys.path.insert(0, str(__import__("pathlib").Path(__file__).parent))
+    from test_checkpoint import _tiny_model
+    from vllm_turing_amd import checkpoint as ck
+    src, dst = tmp_path / "src", tmp_path / "dst"
+    src.mkdir()
+    _tiny_model(str(src))
+    ck.convert(str(src), str(dst), "cuda", None, 0.5, log=lambda *a: None)
+    layers, _ = ck.load(str(dst), device=DEV)
+    g = torch.Generator().manual_seed(8)
+    for name in ("model.language_model.layers.0.mlp.down_proj", "model.language_model.layers.0.self_attn.q_proj"):
+        layer = layers[name]
+        K = layer.weight.shape[1]
+        for M in (3, 64):
+            x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+            out = layer(x.to(DEV))
+            torch.cuda.synchronize()
+            qr, sr = oracle.quant_rows(x)
+            ref, _ = oracle.scaled_mm(qr, layer.weight.cpu().numpy(), sr, layer.weight_scale.cpu().numpy().reshape(-1),
+                                      None, oracle.BF16)
+            assert np.array_equal(bits(out), ref), (name, M)
+
+
 def test_mlp_chain_small(L):
     """gate_up GEMM -> silu_mul_quant -> down GEMM, every intermediate bit-exact (M = 64, the C4 widths)."""
     say("mlp chain")
