@@ -66,6 +66,19 @@ int silu_mul_quant_bf16(const void* gu, void* q, void* scales, int M, int I, voi
 int rms_norm_quant(const void* x, void* residual, const void* weight, const void* scale_ub, float eps, void* q,
                    void* scales, int M, int K, int dtype, void* stream);
 
+/* AR8 group quantization, the compressed operand of the reference's large all-reduce (csrc/host_ar.cu:186-192, same
+ * arguments): x n fp16 (n % 128 == 0) -> packed = n int8 then n / 128 fp16 scales (scale = RN16(absmax / 127) per
+ * 128 values, q = clamp(rint(x / scale), -127, 127)).  Returns 0, -1 on bad arguments, else the HIP launch error. */
+int ar8_quant(const void* x, void* packed, int n, void* stream);
+
+/* The sum of two ranks' dequantised AR8 blocks (csrc/host_ar.cu:194-201, same arguments): gathered = two packed
+ * blocks in rank order (n + n / 64 bytes each) -> out n fp16.  Returns 0, -1 on bad arguments, else the HIP error. */
+int ar8_dequant_sum(const void* gathered, void* out, int n, void* stream);
+
+/* The same for 1..8 ranks in rank order (no counterpart in the reference, which is two-rank only; for the 8 GPUs of
+ * an xGMI node). */
+int ar8_dequant_sum_ranks(const void* gathered, void* out, int n, int ranks, void* stream);
+
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
  * checks: kernel 0 the small-M MFMA streaming kernel (M <= 32), 1 the prefill kernel as dispatched, 2 the v_dot4
  * streaming kernel (M = 1 and K <= 17408, or M = 2 and K <= 8192), 3 and 4 the prefill kernel's quarter-tile and

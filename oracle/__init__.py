@@ -41,6 +41,8 @@ def lib():
         L.o_silu_h.restype = ctypes.c_uint16
         L.o_silu_table.argtypes = [i, vp]
         L.o_silu_mul_quant.argtypes = [vp, i, lg, lg, vp, vp, vp]
+        L.o_ar8_quant.argtypes = [vp, lg, vp]
+        L.o_ar8_dequant_sum.argtypes = [vp, lg, i, vp]
         L.o_rms_norm_quant.argtypes = [vp, vp, vp, vp, ctypes.c_float, lg, lg, i, vp, vp, vp, vp]
         L.o_h2f.argtypes = [ctypes.c_uint16]
         L.o_h2f.restype = ctypes.c_float
@@ -161,6 +163,31 @@ def rms_norm_quant(x, weight, eps, residual=None, scale_ub=None):
     lib().o_rms_norm_quant(_p(xb), None if rb is None else _p(rb), _p(np.ascontiguousarray(wb.reshape(-1))),
                            None if ubv is None else _p(ubv), float(eps), M, K, code, _p(q), _p(s), _p(y), _p(sbuf))
     return q, s, rb, y
+
+
+def ar8_quant(x):
+    """AR8 group quantization (csrc/host_ar.cu:137-164): fp16 [n] (n % 128 == 0) -> packed uint8 [n + n / 64]
+    (n int8 then n / 128 fp16 scales)."""
+    xb, code = _bits(x)
+    if code != FP16:
+        raise TypeError("AR8 takes float16")
+    xb = np.ascontiguousarray(xb.reshape(-1))
+    n = xb.size
+    if n % 128:
+        raise ValueError("n % 128 != 0")
+    packed = np.empty(n + n // 64, np.uint8)
+    lib().o_ar8_quant(_p(xb), n, _p(packed))
+    return packed
+
+
+def ar8_dequant_sum(gathered, n, ranks=2):
+    """Sum of the dequantised packed blocks of `ranks` ranks (csrc/host_ar.cu:166-183) -> fp16 bit patterns [n]."""
+    g = np.ascontiguousarray(np.asarray(gathered, np.uint8).reshape(-1))
+    if g.size != ranks * (n + n // 64):
+        raise ValueError("gathered size")
+    out = np.empty(n, np.uint16)
+    lib().o_ar8_dequant_sum(_p(g), n, ranks, _p(out))
+    return out
 
 
 def scaled_mm(a_q, w_q, sa, sw, bias=None, dtype=FP16, order=None):

@@ -18,6 +18,10 @@
  *                       60 digits and correctly rounded to float32 (the reference's CUDA expf itself cannot be run or
  *                       reproduced; rare 1-ulp differences of CUDA's expf are the one unpinned residue).
  *   o_silu_mul_quant    pinned: composition of the above; the fp16 product is exact IEEE.
+ *   o_ar8_quant / o_ar8_dequant_sum
+ *                       pinned: known groups (exact scales, ties to even, the -127 clamp, zero groups), invariants
+ *                       (|q| <= 127, +-127 at each group's absmax, |x - q s| <= s / 2 in range), the dequantised sum
+ *                       against exact rational arithmetic rounded once to fp16.
  *   o_rms_norm_quant    pinned: residual sum against numpy / torch IEEE conversion, the normalised row against the
  *                       float64 closed form within one 16-bit rounding, rms within 1.5 float32 ulps of the float64
  *                       value, known answers (constant rows -> +-127, zero row -> scale FLT_EPSILON and q = 0) and the
@@ -269,5 +273,53 @@ void o_rms_norm_quant(const uint16_t* x, uint16_t* res, const uint16_t* w, const
         scales[m] = scale;
         const float inv = 1.0f / scale;
         for (long k = 0; k < K; ++k) q[m * K + k] = q8(sbuf[k] * inv);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * AR8: int8 with an fp16 scale per 128-element group, the compressed operand of the reference's large all-reduce
+ * (csrc/host_ar.cu:133-201).  Per group: amax = max|float(x)|, scale = RN16(RN32(amax / 127)), s = float(scale),
+ * inv = s > 0 ? RN32(1 / s) : 0, q = clamp(rint(RN32(float(x) * inv)), -127, 127) (the kernel clamps at -127, not
+ * -128).  packed = n int8 then n / 128 fp16 scales.  x: n fp16 bit patterns, n % 128 == 0.
+ * ------------------------------------------------------------------------------------------------------------------ */
+void o_ar8_quant(const uint16_t* x, long n, uint8_t* packed) {
+    int8_t* q = (int8_t*)packed;
+    uint16_t* sc = (uint16_t*)(packed + n);
+    for (long g = 0; g < n / 128; ++g) {
+        float amax = 0.0f;
+        for (int i = 0; i < 128; ++i) {
+            const float v = fabsf(o_h2f(x[g * 128 + i]));
+            if (v > amax) amax = v;
+        }
+        const uint16_t sh = o_f2h(amax / 127.0f);
+        const float s = o_h2f(sh);
+        const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+        for (int i = 0; i < 128; ++i) {
+            float r = rintf(o_h2f(x[g * 128 + i]) * inv);
+            if (r < -127.0f) r = -127.0f;
+            if (r > 127.0f) r = 127.0f;
+            q[g * 128 + i] = (int8_t)r;
+        }
+        sc[g] = sh;
+    }
+}
+
+/* The sum over `ranks` packed blocks (rank order, each n + n / 64 bytes) of the dequantised values, rounded once to
+ * fp16 (csrc/host_ar.cu:166-183 for two ranks: u * a0 + w * a1, both products exact in float32, one rounding).  For
+ * more ranks the float32 sum runs in rank order, each step a fused multiply-add of an exact product (for two ranks
+ * this is the reference's single rounding). */
+void o_ar8_dequant_sum(const uint8_t* gathered, long n, int ranks, uint16_t* out) {
+    const long m = n + n / 64;
+    for (long i = 0; i < n; ++i) {
+        const long g = i / 128;
+        float acc = 0.0f;
+        for (int r = 0; r < ranks; ++r) {
+            const int8_t* q = (const int8_t*)(gathered + r * m);
+            const uint16_t* sc = (const uint16_t*)(gathered + r * m + n);
+            const float p = (float)q[i] * o_h2f(sc[g]);              /* exact: 8-bit x 11-bit significands */
+            acc = r == 0 ? p : fmaf((float)q[i], o_h2f(sc[g]), acc);
+            (void)p;
+        }
+        out[i] = o_f2h(acc);
     }
 }

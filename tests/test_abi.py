@@ -69,6 +69,11 @@ def test_argument_validation_codes(L):
     assert L.per_token_quant(None, None, None, 4, 16, 16, 0, None) == -1
     assert L.per_token_quant(16, 16, 16, 0, 16, 16, 0, None) == 0
     assert L.silu_table(None, 0, None) == -1
+    assert L.ar8_quant(16, 16, 100, None) == -1                                 # n % 128
+    assert L.ar8_quant(8, 16, 128, None) == -1                                  # x 16-byte aligned
+    assert L.ar8_quant(16, 16, 0, None) == 0
+    assert L.ar8_dequant_sum_ranks(16, 16, 128, 9, None) == -1                  # 1..8 ranks
+    assert L.ar8_dequant_sum(16, 16, 130, None) == -1
     assert L.f32_to_16(None, None, 4, 1, None) == -1
     assert L.f32_to_16(16, 16, 4, 2, None) == -1
     assert L.f32_to_16(16, 16, 0, 1, None) == 0

@@ -94,6 +94,61 @@ def test_device_rounding(L, dt):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# AR8 group quant / dequantised rank sum
+# ---------------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [128, 128 * 7, 4096 * 5120, 128 * 1001])
+def test_ar8_quant(L, n):
+    say(f"ar8_quant n={n}")
+    g = torch.Generator().manual_seed(n % 9973)
+    x = torch.randn(n, generator=g) * torch.rand(n // 128, generator=g).repeat_interleave(128) * 50
+    x = x.half()
+    if n >= 128 * 7:
+        x[128:256] = 0                                     # a zero group
+        x[300] = 65504.0                                   # the largest fp16
+        x[600:610] = 1e-6                                  # subnormals
+    xd = x.to(DEV)
+    packed = torch.empty(n + n // 64, dtype=torch.uint8, device=DEV)
+    assert L.ar8_quant(xd.data_ptr(), packed.data_ptr(), n, stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(packed.cpu().numpy(), oracle.ar8_quant(x))
+
+
+@pytest.mark.parametrize("ranks", [1, 2, 3, 8])
+def test_ar8_dequant_sum(L, ranks):
+    say(f"ar8_dequant_sum ranks={ranks}")
+    from vllm_turing_amd import ar8
+    n = 128 * 2000
+    g = torch.Generator().manual_seed(ranks)
+    xs = [(torch.randn(n, generator=g) * 3).half() for _ in range(ranks)]
+    gathered = torch.cat([ar8.ar8_quant(x.to(DEV)) for x in xs])
+    out = ar8.ar8_dequant_sum(gathered, n, ranks)
+    if ranks == 2:                                         # the reference's two-rank entry point
+        out2 = torch.empty(n, dtype=torch.float16, device=DEV)
+        assert L.ar8_dequant_sum(gathered.data_ptr(), out2.data_ptr(), n, stream()) == 0
+        assert torch.equal(out, out2)
+    torch.cuda.synchronize()
+    ref = oracle.ar8_dequant_sum(np.concatenate([oracle.ar8_quant(x) for x in xs]), n, ranks)
+    assert np.array_equal(bits(out), ref)
+    # a lossy all-reduce: within half a scale step per rank of the exact sum
+    exact = torch.stack([x.float() for x in xs]).sum(0)
+    step = sum(x.float().view(-1, 128).abs().amax(1).repeat_interleave(128) / 127 for x in xs)
+    assert torch.all((out.cpu().float() - exact).abs() <= step * 0.51 + exact.abs() * 1e-3 + 1e-3)
+
+
+def test_ar8_all_reduce_composition(L):
+    """ar8_all_reduce with the all-gather of two 'ranks' simulated on one GPU: every rank gets the same sum."""
+    say("ar8_all_reduce")
+    from vllm_turing_amd import ar8
+    g = torch.Generator().manual_seed(77)
+    a, b = (torch.randn(64, 5120, generator=g).half().to(DEV) for _ in range(2))
+    other = ar8.ar8_quant(b)
+    r0 = ar8.ar8_all_reduce(a, lambda p: torch.cat([p, other]), 2)
+    r1 = ar8.ar8_all_reduce(b, lambda p: torch.cat([ar8.ar8_quant(a), p]), 2)
+    torch.cuda.synchronize()
+    assert r0.shape == a.shape and torch.equal(r0, r1)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # residual add + RMSNorm + per-token quant
 # ---------------------------------------------------------------------------------------------------------------------
 RNQ_CASES = [(1, 5120), (7, 5120), (300, 5120), (4, 17408), (3, 6144), (2, 136), (5, 8), (3, 5001), (2, 65536),

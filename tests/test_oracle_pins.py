@@ -10,6 +10,7 @@ int32 -> float conversion, a missed zero-row rule) fails it:
   * epilogues: exact rational arithmetic (fractions.Fraction) with correct rounding at each step the reference
     rounds, plus the float64 closed form of the reference's own test (tests/test_w8a8_mma.py:43-51);
   * per-token quant: hand-computed known answers, invariants, and a case where x / scale differs from x * inverse;
+  * AR8 group quant: exact scales, ties to even, invariants, and the dequantised rank sum against exact rationals;
   * residual add + RMSNorm + quant: the residual against torch's IEEE float32 add and RN conversion, the normalised
     row against the float64 closed form within one 16-bit ulp, constant and zero rows, the scale bound, invariants.
 """
@@ -432,3 +433,58 @@ def test_rms_norm_quant_scale_bound(oracle_lib):
     inv = np.float32(1) / s2
     yv = torch.from_numpy(y2.view(np.int16)).view(torch.float16).float().numpy()
     assert np.array_equal(q2, np.clip(np.rint(yv * inv[:, None]), -128, 127).astype(np.int8))
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# AR8: int8 + fp16 scale per 128-element group (csrc/host_ar.cu:133-201)
+# ---------------------------------------------------------------------------------------------------------------------
+def test_ar8_known_group(oracle_lib):
+    x = np.zeros(256, np.float16)
+    x[0] = 127.0                                           # group 0: absmax 127 -> scale exactly 1, inverse 1
+    x[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, 3.49, -126.5, 63.5]
+    p = oracle.ar8_quant(x)
+    q = p[:256].view(np.int8)
+    sc = p[256:].view(np.float16)
+    assert sc[0] == 1.0 and sc[1] == 0.0                   # group 1 is all zero: scale 0 and q = 0
+    assert q[:9].tolist() == [127, 0, 2, 2, 0, -2, 3, -126, 64]
+    assert np.all(q[128:] == 0)
+
+
+def test_ar8_invariants(oracle_lib):
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(128 * 64, generator=g) * torch.rand(64, generator=g).repeat_interleave(128) * 30).half()
+    x[5 * 128:6 * 128] = 0
+    p = oracle.ar8_quant(x)
+    n = x.numel()
+    q = p[:n].view(np.int8).astype(np.int32).reshape(-1, 128)
+    sc = p[n:].view(np.float16).astype(np.float32)
+    xf = x.float().numpy().reshape(-1, 128)
+    amax = np.abs(xf).max(axis=1)
+    assert np.array_equal(sc, (amax / np.float32(127)).astype(np.float16).astype(np.float32))   # RN16(amax / 127)
+    assert q.min() >= -127 and q.max() <= 127
+    nz = amax > 0
+    assert np.all(np.abs(q[nz][np.arange(nz.sum()), np.abs(xf[nz]).argmax(axis=1)]) == 127)
+    err = np.abs(xf - q * sc[:, None])
+    assert np.all(err <= sc[:, None] / 2 * (1 + 1e-6) + 1e-12)
+
+
+def test_ar8_dequant_sum_exact(oracle_lib):
+    g = torch.Generator().manual_seed(22)
+    n = 128 * 6
+    xs = [(torch.randn(n, generator=g) * 4).half() for _ in range(3)]
+    packed = [oracle.ar8_quant(x) for x in xs]
+    for ranks in (1, 2, 3):
+        out = oracle.ar8_dequant_sum(np.concatenate(packed[:ranks]), n, ranks)
+        for i in list(range(0, n, 37)) + [n - 1]:
+            terms = []
+            for r in range(ranks):
+                q = int(packed[r][i].astype(np.int8))
+                s = Fraction(float(packed[r][n:].view(np.float16)[i // 128]))
+                terms.append(q * s)
+            if ranks <= 2:                                 # one rounding of the exact sum to float32, then to fp16
+                acc = rn_bin(sum(terms), F32)
+            else:                                          # rank order, each step rounded to float32
+                acc = terms[0]
+                for t in terms[1:]:
+                    acc = rn_bin(acc + t, F32)
+            assert int(out[i]) == f16_bits(rn_bin(acc, F16)), (ranks, i)

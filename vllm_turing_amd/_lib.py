@@ -17,6 +17,9 @@ SIGNATURES = {
     "per_token_quant": [_vp] * 3 + [_i, _i, _l, _i, _vp],
     "silu_mul_quant": [_vp] * 3 + [_i] * 2 + [_vp],
     "silu_mul_quant_bf16": [_vp] * 3 + [_i] * 2 + [_vp],
+    "ar8_quant": [_vp, _vp, _i, _vp],
+    "ar8_dequant_sum": [_vp, _vp, _i, _vp],
+    "ar8_dequant_sum_ranks": [_vp, _vp, _i, _i, _vp],
     "rms_norm_quant": [_vp] * 4 + [ctypes.c_float] + [_vp] * 2 + [_i] * 3 + [_vp],
     "w8a8_i32": [_vp] * 3 + [_i] * 4 + [_vp],
     "silu_table": [_vp, _i, _vp],
