@@ -10,7 +10,8 @@ is GPU work only (HIP events on the launch stream, bracketed by synchronizations
 Also reported:
   decode_other_m: the same GEMV at M = 2, 4, 8;
   gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline);
-  quant: per-token quant at M=4096, K=5120 and SiLU*up+quant at M=4096, I=17408, in GB/s (HBM-bound);
+  quant: per-token quant at M=4096, K=5120, SiLU*up+quant at M=4096, I=17408, and the AR8 all-reduce operand
+    (quantize; dequantised sum of 2 and 8 ranks) at 4096 x 5120, in GB/s (HBM-bound);
   cpu_baseline: the reference's CPU path restated (oracle/cpu_path.py: torch CPU int8 matmul + dequant), timed on a
     bounded sample on this host's cores;
   mlp_chain: the fused MLP tail at M=4096 as the reference runs it (residual add + RMSNorm + int8 quant -> gate_up
@@ -382,6 +383,33 @@ def bench_headline(torch, L, st, dev, args):
     smq_bytes = 2 * Mg * 2 * I + Mg * I + 4 * Mg
     print(f"[bench] quant {ms_q * 1e3:.1f} us, silu_mul_quant {ms_s * 1e3:.1f} us", file=sys.stderr, flush=True)
 
+    # AR8 operand of a prefill-size all-reduce (4096 x 5120 fp16): quantize, and the dequantised sum of 2 / 8 ranks
+    n8 = Mg * Kg
+    a8 = torch.randn(n8, device=dev).half()
+    p8 = torch.empty(8 * (n8 + n8 // 64), dtype=torch.uint8, device=dev)
+    o8 = torch.empty(n8, dtype=torch.float16, device=dev)
+    for r in range(8):
+        L.ar8_quant(a8.data_ptr(), p8.data_ptr() + r * (n8 + n8 // 64), n8, st())
+
+    def ar8q(i):
+        if L.ar8_quant(a8.data_ptr(), p8.data_ptr(), n8, st()) != 0:
+            raise RuntimeError("ar8_quant")
+
+    ar8_res = {}
+    ms_a, _ = graph_time(torch, ar8q, 10, 200, 20)
+    b_a = 2 * n8 + n8 + n8 // 64
+    ar8_res["quant_us"], ar8_res["quant_gbs"] = round(ms_a * 1e3, 2), round(b_a / ms_a / 1e6, 1)
+    for ranks in (2, 8):
+        def ar8s(i, ranks=ranks):
+            if L.ar8_dequant_sum_ranks(p8.data_ptr(), o8.data_ptr(), n8, ranks, st()) != 0:
+                raise RuntimeError("ar8_dequant_sum")
+        ms_d, _ = graph_time(torch, ar8s, 10, 200, 20)
+        b_d = ranks * (n8 + n8 // 64) + 2 * n8
+        ar8_res[f"dequant_sum_{ranks}ranks_us"] = round(ms_d * 1e3, 2)
+        ar8_res[f"dequant_sum_{ranks}ranks_gbs"] = round(b_d / ms_d / 1e6, 1)
+    del a8, p8, o8
+    print(f"[bench] AR8 n={n8}: {ar8_res}", file=sys.stderr, flush=True)
+
     # ---- CPU baseline: the reference's CPU path (torch int8 matmul + dequant), bounded sample ---------------------
     cpu = None
     cpu_gemm = None
@@ -430,7 +458,8 @@ def bench_headline(torch, L, st, dev, args):
         "quant": {"per_token_quant_M4096_K5120": {"us": round(ms_q * 1e3, 2),
                                                    "gbs": round(quant_bytes / (ms_q * 1e-3) / 1e9, 1)},
                   "silu_mul_quant_M4096_I17408": {"us": round(ms_s * 1e3, 2),
-                                                   "gbs": round(smq_bytes / (ms_s * 1e-3) / 1e9, 1)}},
+                                                   "gbs": round(smq_bytes / (ms_s * 1e-3) / 1e9, 1)},
+                  "ar8_n20971520": ar8_res},
     }
     return result
 
