@@ -79,6 +79,18 @@ int ar8_dequant_sum(const void* gathered, void* out, int n, void* stream);
  * an xGMI node). */
 int ar8_dequant_sum_ranks(const void* gathered, void* out, int n, int ranks, void* stream);
 
+/* The int8 LM head, W8A16 (csrc/w8a16_gemv.cu:145-154, same arguments): out [M, N] = x [M, K] (fp16 dtype 0 / bf16
+ * dtype 1) times the int8 rows w [N, K] with float32 per-row scales s [N] and an optional bias [N] of the activation
+ * type: RN(fma(sum_k w x, s, bias)) with float32 sums.  M in 1..32 (the reference: 1..16), K % 16 == 0.  Returns -1 on
+ * bad arguments, else the HIP launch error. */
+int w8a16_gemv(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K, int dtype,
+               void* stream);
+
+/* The same over the gathered weight rows rows[0..N) (int32, indexes into the w_rows rows of w; out is compact), as
+ * csrc/w8a16_gemv.cu:145-146 for a pruned draft vocabulary; w_rows bounds the reads and has no counterpart there. */
+int w8a16_gemv_rows(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
+                    int dtype, const void* rows, int w_rows, void* stream);
+
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
  * checks: kernel 0 the small-M MFMA streaming kernel (M <= 32), 1 the prefill kernel as dispatched, 2 the v_dot4
  * streaming kernel (M = 1 and K <= 17408, or M = 2 and K <= 8192), 3 and 4 the prefill kernel's quarter-tile and

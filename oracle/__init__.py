@@ -41,6 +41,7 @@ def lib():
         L.o_silu_h.restype = ctypes.c_uint16
         L.o_silu_table.argtypes = [i, vp]
         L.o_silu_mul_quant.argtypes = [vp, i, lg, lg, vp, vp, vp]
+        L.o_w8a16.argtypes = [vp, vp, vp, vp, vp, vp, lg, lg, lg, i]
         L.o_ar8_quant.argtypes = [vp, lg, vp]
         L.o_ar8_dequant_sum.argtypes = [vp, lg, i, vp]
         L.o_rms_norm_quant.argtypes = [vp, vp, vp, vp, ctypes.c_float, lg, lg, i, vp, vp, vp, vp]
@@ -163,6 +164,26 @@ def rms_norm_quant(x, weight, eps, residual=None, scale_ub=None):
     lib().o_rms_norm_quant(_p(xb), None if rb is None else _p(rb), _p(np.ascontiguousarray(wb.reshape(-1))),
                            None if ubv is None else _p(ubv), float(eps), M, K, code, _p(q), _p(s), _p(y), _p(sbuf))
     return q, s, rb, y
+
+
+def w8a16(x, w, s, bias=None, rows=None):
+    """The int8 LM head (csrc/w8a16_gemv.cu:98-117): x fp16/bf16 [M, K], w int8 [w_rows, K], s float32 [w_rows],
+    bias [w_rows] of x's dtype or None, rows int32 [N] or None -> out bit patterns uint16 [M, N] (float64 sums rounded
+    once to float32, then fma with the scale and bias and one rounding to the 16-bit type)."""
+    xb, code = _bits(x)
+    M, K = xb.shape
+    w = np.ascontiguousarray(np.asarray(w, np.int8))
+    s = np.ascontiguousarray(np.asarray(s, np.float32).reshape(-1))
+    r = None if rows is None else np.ascontiguousarray(np.asarray(rows, np.int32).reshape(-1))
+    N = w.shape[0] if r is None else r.size
+    b = None
+    if bias is not None:
+        b, bcode = _bits(bias)
+        b = np.ascontiguousarray(b.reshape(-1))
+    out = np.empty((M, N), np.uint16)
+    lib().o_w8a16(_p(xb), _p(w), _p(s), None if b is None else _p(b), None if r is None else _p(r), _p(out), M, N, K,
+                  code)
+    return out
 
 
 def ar8_quant(x):

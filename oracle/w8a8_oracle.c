@@ -18,6 +18,9 @@
  *                       60 digits and correctly rounded to float32 (the reference's CUDA expf itself cannot be run or
  *                       reproduced; rare 1-ulp differences of CUDA's expf are the one unpinned residue).
  *   o_silu_mul_quant    pinned: composition of the above; the fp16 product is exact IEEE.
+ *   o_w8a16             pinned: the float64 closed form (x . (w s)^T + bias) within one 16-bit rounding plus the float32
+ *                       sum's error bound; gathered rows against the dense result; the sum order is the kernel's own
+ *                       (float32 MFMA), so the GPU is compared to tolerance, as the reference's own head is.
  *   o_ar8_quant / o_ar8_dequant_sum
  *                       pinned: known groups (exact scales, ties to even, the -127 clamp, zero groups), invariants
  *                       (|q| <= 127, +-127 at each group's absmax, |x - q s| <= s / 2 in range), the dequantised sum
@@ -321,5 +324,24 @@ void o_ar8_dequant_sum(const uint8_t* gathered, long n, int ranks, uint16_t* out
             (void)p;
         }
         out[i] = o_f2h(acc);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * The int8 LM head (W8A16), csrc/w8a16_gemv.cu:98-117: out[m, n] = RN_T( fmaf( acc, s[row], b ) ), acc the float32 sum
+ * of float(w[row, k]) * float(x[m, k]) over k, b = float(bias[row]) or +0, row = rows ? rows[n] : n.  The reference
+ * sums in its own lane order; here acc is the float64 sum (every product exact) rounded once to float32, the value any
+ * summation order approximates.  x: [M, K] bit patterns of dtype; w: int8 [w_rows, K]; s: [w_rows]; out: [M, N].
+ * ------------------------------------------------------------------------------------------------------------------ */
+void o_w8a16(const uint16_t* x, const int8_t* w, const float* s, const uint16_t* bias, const int32_t* rows,
+             uint16_t* out, long M, long N, long K, int dtype) {
+    for (long m = 0; m < M; ++m) {
+        for (long n = 0; n < N; ++n) {
+            const long row = rows ? rows[n] : n;
+            double acc = 0.0;
+            for (long k = 0; k < K; ++k) acc += (double)w[row * K + k] * (double)to_f(x[m * K + k], dtype);
+            const float b = bias ? to_f(bias[row], dtype) : 0.0f;
+            out[m * N + n] = from_f(fmaf((float)acc, s[row], b), dtype);
+        }
     }
 }

@@ -69,6 +69,10 @@ def test_argument_validation_codes(L):
     assert L.per_token_quant(None, None, None, 4, 16, 16, 0, None) == -1
     assert L.per_token_quant(16, 16, 16, 0, 16, 16, 0, None) == 0
     assert L.silu_table(None, 0, None) == -1
+    assert L.w8a16_gemv(16, 16, 16, None, 16, 33, 64, 64, 0, None) == -1        # M <= 32
+    assert L.w8a16_gemv(16, 16, 16, None, 16, 4, 64, 72, 0, None) == -1         # K % 16
+    assert L.w8a16_gemv(16, 16, 16, None, 16, 4, 64, 64, 2, None) == -1         # dtype
+    assert L.w8a16_gemv_rows(16, 16, 16, None, 16, 4, 64, 64, 0, None, 64, None) == -1   # rows required
     assert L.ar8_quant(16, 16, 100, None) == -1                                 # n % 128
     assert L.ar8_quant(8, 16, 128, None) == -1                                  # x 16-byte aligned
     assert L.ar8_quant(16, 16, 0, None) == 0

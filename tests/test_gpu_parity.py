@@ -94,6 +94,76 @@ def test_device_rounding(L, dt):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# int8 LM head (W8A16): float32 sums in the kernel's own order, so to tolerance against the oracle's float64 sum
+# ---------------------------------------------------------------------------------------------------------------------
+def _ulp16_t(v, dt):
+    mant, emin = (10, -14) if dt == torch.float16 else (7, -126)
+    e = torch.floor(torch.log2(torch.clamp(v.abs(), min=2.0 ** emin)))
+    return 2.0 ** (e - mant)
+
+
+W8A16_CASES = [(1, 17408, 5120), (4, 4096, 5120), (16, 1000, 2048), (5, 333, 4112), (32, 2048, 1024), (17, 64, 16),
+               (3, 248320 // 8, 5120)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", W8A16_CASES)
+def test_w8a16(L, dt, M, N, K):
+    say(f"w8a16 M={M} N={N} K={K} {dt}")
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(dt)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    s = (torch.rand(N, generator=g) * 2e-3 + 1e-4).float()
+    bias = torch.randn(N, generator=g).to(dt) if N % 2 else None
+    out = torch.empty(M, N, dtype=dt, device=DEV)
+    xd, wd, sd = x.to(DEV), w.to(DEV), s.to(DEV)                  # kept alive until the kernel has run
+    bd = bias.to(DEV) if bias is not None else None
+    rc = L.w8a16_gemv(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr() if bd is not None else None,
+                      out.data_ptr(), M, N, K, code(dt), stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(oracle.w8a16(x, w.numpy(), s.numpy(), bias).view(np.int16)).view(dt).double()
+    got = out.cpu().double()
+    # float32 sums in another order than the oracle's (float64, rounded once): at most one 16-bit step apart plus the
+    # float32 summation error bound K u sum|w x| s, which dominates where the logit cancels to near zero
+    absdot = (x.double().abs() @ w.double().abs().T) * s.double()
+    bound = _ulp16_t(ref, dt) * 1.0001 + K * 2.0 ** -24 * absdot
+    over = (got - ref).abs() > bound
+    assert not over.any(), f"{over.sum().item()} outputs outside the bound"
+    assert (got == ref).double().mean() > 0.97
+    # and the reference head's own criterion against the float64 closed form (rel <= 1e-3 of the logit scale)
+    exact = (x.double() @ w.double().T) * s.double() + (bias.double() if bias is not None else 0)
+    assert ((got - exact).abs() / (exact.abs() + 1e-3 * exact.abs().max())).max() < 1e-2 if dt == torch.bfloat16 \
+        else ((got - exact).abs() / (exact.abs() + 1e-3 * exact.abs().max())).max() < 2e-3
+
+
+def test_w8a16_rows_and_api(L):
+    say("w8a16 rows + api")
+    from vllm_turing_amd import lmhead
+    g = torch.Generator().manual_seed(3)
+    N, K = 3000, 5120
+    w16 = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    wq, ws = lmhead.quantize_rows(w16.to(DEV))
+    # torch divides a GPU tensor by a Python scalar as a multiply by the float32 reciprocal (on CUDA as on ROCm, so the
+    # reference's own conversion does the same): scale = amax * RN32(1 / 127), then a true tensor division
+    sc = w16.float().abs().amax(1).clamp(min=1e-12) * torch.tensor(1 / 127, dtype=torch.float32)
+    assert torch.equal(ws.cpu(), sc)
+    wq_ref = torch.round(w16.float() / sc[:, None]).clamp(-128, 127)
+    assert torch.equal(wq.cpu(), wq_ref.to(torch.int8))
+    x = torch.randn(2, 7, K, generator=g).to(torch.bfloat16)          # 14 rows, leading dims kept
+    y = lmhead.w8a16_mm(x.to(DEV), wq, ws)
+    rows = torch.tensor([2999, 0, 17, 17, 1234], dtype=torch.int32)
+    yr = lmhead.w8a16_mm_rows(x.to(DEV), wq, ws, rows.to(DEV))
+    x40 = torch.randn(40, K, generator=g).to(torch.bfloat16)           # two kernel passes (32 + 8 rows)
+    y40 = lmhead.w8a16_mm(x40.to(DEV), wq, ws)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 7, N)
+    assert torch.equal(yr.cpu(), y.reshape(14, N)[:, rows.long()].cpu())
+    ref40 = torch.from_numpy(oracle.w8a16(x40, wq.cpu().numpy(), ws.cpu().numpy()).view(np.int16)).view(torch.bfloat16)
+    assert (y40.cpu() == ref40).double().mean() > 0.97
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # AR8 group quant / dequantised rank sum
 # ---------------------------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("n", [128, 128 * 7, 4096 * 5120, 128 * 1001])

@@ -10,6 +10,7 @@ int32 -> float conversion, a missed zero-row rule) fails it:
   * epilogues: exact rational arithmetic (fractions.Fraction) with correct rounding at each step the reference
     rounds, plus the float64 closed form of the reference's own test (tests/test_w8a8_mma.py:43-51);
   * per-token quant: hand-computed known answers, invariants, and a case where x / scale differs from x * inverse;
+  * int8 LM head (W8A16): the float64 closed form within one 16-bit rounding; gathered rows against the dense result;
   * AR8 group quant: exact scales, ties to even, invariants, and the dequantised rank sum against exact rationals;
   * residual add + RMSNorm + quant: the residual against torch's IEEE float32 add and RN conversion, the normalised
     row against the float64 closed form within one 16-bit ulp, constant and zero rows, the scale bound, invariants.
@@ -488,3 +489,28 @@ def test_ar8_dequant_sum_exact(oracle_lib):
                 for t in terms[1:]:
                     acc = rn_bin(acc + t, F32)
             assert int(out[i]) == f16_bits(rn_bin(acc, F16)), (ranks, i)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# int8 LM head, W8A16 (csrc/w8a16_gemv.cu)
+# ---------------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_w8a16_closed_form(oracle_lib, dt):
+    g = torch.Generator().manual_seed(31)
+    M, N, K = 3, 200, 1024
+    x = torch.randn(M, K, generator=g).to(dt)
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, generator=g)
+    s = (torch.rand(N, generator=g) * 1e-3 + 1e-4).float()
+    bias = torch.randn(N, generator=g).to(dt)
+    out = oracle.w8a16(x, w.numpy(), s.numpy(), bias)
+    ref = (x.double() @ w.double().T) * s.double() + bias.double()
+    got = torch.from_numpy(out.view(np.int16)).view(dt).double()
+    # one rounding to the 16-bit type after the float32 steps (the float64 sum rounded to float32, one fma)
+    assert torch.all((got - ref).abs() <= torch.from_numpy(_ulp16(ref.numpy(), dt)) * 0.5001 + ref.abs() * 2 ** -22)
+    # without a bias: fma with +0, i.e. the rounded product
+    out0 = oracle.w8a16(x, w.numpy(), s.numpy())
+    ref0 = ((x.double() @ w.double().T).float() * s).to(dt)
+    assert np.array_equal(out0, ref0.view(torch.int16).numpy().view(np.uint16))
+    # gathered rows = the same columns of the dense result
+    rows = np.array([199, 0, 57, 57, 3], np.int32)
+    assert np.array_equal(oracle.w8a16(x, w.numpy(), s.numpy(), bias, rows), out[:, rows])

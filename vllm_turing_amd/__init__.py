@@ -7,6 +7,8 @@ C ABI (include/w8a8_mi355.h) loaded with ctypes, and Python hooks with the refer
   quantfuse.scaled_int8_quant / quant_torch                         (vllm_turing/quantfuse.py)
   tailoverlap.silu_mul_quant / mlp_tail                             (vllm_turing/tailoverlap.py)
   normquant.rms_norm_dynamic_per_token_quant                        (vLLM's fused op, tailoverlap.py:145)
+  lmhead.w8a16_mm / quantize_rows                                   (vllm_turing/lmhead.py, the int8 LM head)
+  ar8.ar8_quant / ar8_dequant_sum                                   (vllm_turing/hostar.py, AR8 operand)
 register() mirrors the reference plugin entry point (vllm_turing/__init__.py:38-72): with vLLM importable on a gfx950
 device it patches vllm._custom_ops; VLLM_TURING_DISABLE=1 turns it off.  Importing the package builds nothing; the
 library is built or loaded on first use.
@@ -17,7 +19,7 @@ import os
 logger = logging.getLogger("vllm.turing_amd")
 _registered = False
 
-from . import normquant, quantfuse, w8a8  # noqa: E402  (defines the custom ops)
+from . import ar8, lmhead, normquant, quantfuse, w8a8  # noqa: E402,F401  (defines the custom ops)
 from .linear import W8A8Linear, W8A8LinearMethod  # noqa: E402,F401
 from .normquant import rms_norm_dynamic_per_token_quant  # noqa: E402,F401
 from .quantfuse import per_token_quant, quant_torch, scaled_int8_quant  # noqa: E402,F401
@@ -34,6 +36,7 @@ def register():
     q = quantfuse.install()
     n = normquant.install()
     m = w8a8.install()
+    lmhead.install()
     logger.info("vllm_turing_amd: scaled_int8_quant hook %s, rms_norm_dynamic_per_token_quant hook %s, "
                 "cutlass_scaled_mm hook %s (GEMV up to M=%d)", "on" if q else "off", "on" if n else "off",
                 "on" if m else "off", w8a8.MAX_M)

@@ -17,6 +17,8 @@ SIGNATURES = {
     "per_token_quant": [_vp] * 3 + [_i, _i, _l, _i, _vp],
     "silu_mul_quant": [_vp] * 3 + [_i] * 2 + [_vp],
     "silu_mul_quant_bf16": [_vp] * 3 + [_i] * 2 + [_vp],
+    "w8a16_gemv": [_vp] * 5 + [_i] * 4 + [_vp],
+    "w8a16_gemv_rows": [_vp] * 5 + [_i] * 4 + [_vp, _i, _vp],
     "ar8_quant": [_vp, _vp, _i, _vp],
     "ar8_dequant_sum": [_vp, _vp, _i, _vp],
     "ar8_dequant_sum_ranks": [_vp, _vp, _i, _i, _vp],

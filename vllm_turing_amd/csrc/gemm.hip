@@ -6,7 +6,7 @@
 // it, passed to cutlass_scaled_mm as its [K, N] stride-(1, K) view); sa: float32 [M] or [1]; sw: float32 [N] or [1];
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
-// Three kernels:
+// Four kernels:
 //  * gemv_dot4_kernel, M = 1 and K <= 17408, or M = 2 and K <= 8192 (decode): weight-streaming through the VALU: each
 //    wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in
 //    registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
@@ -15,6 +15,8 @@
 //    by direct-to-LDS loads of 1 KB (8 rows x 128 contiguous bytes each), and feed v_mfma_i32_16x16x64_i8 with the
 //    weights as the A operand and up to 16 activation rows per MFMA as the B operand.  The K slices of a tile meet in
 //    LDS.  Small-M epilogue chain.
+//  * w8a16_kernel (the int8 LM head: fp16 / bf16 activations, M <= 32): the LDS-ring weight stream with each int8
+//    fragment widened to fp16 / bf16 in registers for v_mfma_f32_16x16x32_{f16,bf16}; float32 sums.
 //  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
 //    each a 4 x 2 grid of v_mfma_i32_32x32x32_i8; 128-byte K stages loaded straight from HBM into LDS
 //    (buffer_load ... lds), double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128
@@ -556,6 +558,138 @@ __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restric
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// w8a16_kernel: int8 weights (per-row float32 scale) x fp16 / bf16 activations, the int8 LM head, M <= 16 * MT rows
+// ---------------------------------------------------------------------------------------------------------------------
+// out[m, n] = RN_T( fma( sum_k float(w[n, k]) * float(x[m, k]), s[n], bias[n] or +0 ) )   (csrc/w8a16_gemv.cu:98-117,
+// float32 sums; the order of the sum is this kernel's own: the MFMA's and then the 4 K slices in order).
+// The weight stream is the LDS-ring design of stream_lds_kernel (16 weight rows per workgroup, 4 wavefronts on
+// interleaved 128-byte K steps, direct-to-LDS loads of 8 rows x 128 bytes); each 8-byte weight fragment is widened to
+// 8 fp16 / bf16 values in registers and fed to v_mfma_f32_16x16x32_{f16,bf16} as the A operand, the activations
+// (read from L2, 16 bytes per lane) as the B operand.  GATHER: weight rows rows[n] (a gathered vocabulary subset).
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bh8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// 8 int8 -> 8 fp16, exact: byte b becomes the fp16 with bits 0x6400 | (b ^ 0x80), i.e. 1024 + (b + 128), minus 1152.
+__device__ __forceinline__ h8 widen_f16(uint32_t lo, uint32_t hi) {
+    const uint32_t a = lo ^ 0x80808080u, b = hi ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) - bias;
+    const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) - bias;
+    const h2 p2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) - bias;
+    const h2 p3 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) - bias;
+    return h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+// 8 int8 -> 8 bf16, exact: through float32 (|b| <= 128 fits the 8-bit bf16 significand, so the high half is exact).
+__device__ __forceinline__ bh8 widen_bf16(uint32_t lo, uint32_t hi) {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t src = i < 2 ? lo : hi;
+        const float f0 = (float)(int8_t)((src >> (16 * (i & 1))) & 0xff);
+        const float f1 = (float)(int8_t)((src >> (16 * (i & 1) + 8)) & 0xff);
+        o[i] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    }
+    return __builtin_bit_cast(bh8, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+template <typename T, int MT, int NS, bool GATHER>
+__global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                    const float* __restrict__ s, const uint16_t* __restrict__ bias,
+                                                    uint16_t* __restrict__ out, int M, int N, int K, int w_rows,
+                                                    const int* __restrict__ rows) {
+    constexpr int KS = 4, STEP_BYTES = 16 * 128, LPS = 2;
+    extern __shared__ v4i ldsx[];
+    const int ks = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = blockIdx.x * 16;
+    uint8_t* const ring = reinterpret_cast<uint8_t*>(ldsx) + ks * NS * STEP_BYTES;
+    const __amdgpu_buffer_rsrc_t rsw = make_rsrc(w, (long)w_rows * K);
+    int off[LPS], chk[LPS];
+#pragma unroll
+    for (int j = 0; j < LPS; ++j) {
+        const int row = j * 8 + (lane >> 3);
+        chk[j] = (lane & 7) ^ swz<8>(row);
+        const int n = n0 + row;
+        const int src = n < N ? (GATHER ? min(max(rows[n], 0), w_rows - 1) : n) : 0;   // a bad index stays in w
+        off[j] = n < N ? src * K + chk[j] * 16 : 0x7fffffff;
+    }
+    const int nsteps = (K + 127) >> 7;
+    const int mine = ks < nsteps ? (nsteps - 1 - ks) / KS + 1 : 0;
+    auto issue = [&](int i) {
+        dma_step(rsw, rsw, ring + (i % NS) * STEP_BYTES, off, chk, LPS, (ks + i * KS) * 128, K);
+    };
+    f4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int r = lane & 15, g = lane >> 4;
+    auto compute = [&](int slot, int k0) {
+        const uint8_t* st = ring + slot * STEP_BYTES;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {                    // 32-element MFMA K blocks of the 128-byte step
+            const int c = 2 * j + (g >> 1);
+            const uint2 wv = *reinterpret_cast<const uint2*>(st + r * 128 + (c ^ swz<8>(r)) * 16 + 8 * (g & 1));
+            const int k = k0 + 32 * j + 8 * g;           // this lane's 8 activations
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mt * 16 + r;
+                const uint4 xv = m < M && k < K ? *reinterpret_cast<const uint4*>(x + (long)m * K + k)
+                                                : make_uint4(0, 0, 0, 0);
+                if constexpr (__is_same(T, f16))
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(widen_f16(wv.x, wv.y),
+                                                                     __builtin_bit_cast(h8, xv), acc[mt], 0, 0, 0);
+                else
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(widen_bf16(wv.x, wv.y),
+                                                                      __builtin_bit_cast(bh8, xv), acc[mt], 0, 0, 0);
+            }
+        }
+    };
+    constexpr int WAIT2 = waitcnt_vm(2 * LPS), WAIT1 = waitcnt_vm(LPS), WAIT0 = waitcnt_vm(0);
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < mine) issue(i);
+    for (int i = 0; i < mine; ++i) {
+        const int ahead = min(mine - 1 - i, NS - 2);
+        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAIT1);
+        else __builtin_amdgcn_s_waitcnt(WAIT0);
+        if (i + NS - 1 < mine) issue(i + NS - 1);
+        compute(i % NS, (ks + i * KS) * 128);
+    }
+    // K slices meet in LDS, in slice order
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(ldsx) + lane;
+    if (ks > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[((ks - 1) * MT * 4 + mt * 4 + v) * 64] = acc[mt][v];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int q = 0; q < KS - 1; ++q)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[mt][v] += red[(q * MT * 4 + mt * 4 + v) * 64];
+    // D of v_mfma_f32_16x16x32: lane holds rows 4 g + v (weight rows) of column r (activation row)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int n = n0 + 4 * g + v;
+            if (n >= N) continue;
+            const int src = GATHER ? min(max(rows[n], 0), w_rows - 1) : n;
+            const float b = bias ? to_float(T{bias[src]}) : 0.0f;
+            out[(long)m * N + n] = from_float<T>(__builtin_fmaf(acc[mt][v], s[src], b));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------------------------------
 struct Args {
@@ -791,4 +925,55 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
         launch_dot4<f16, EPI_I32>(p);
     }
     return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// W8A16 (int8 LM head)
+// ---------------------------------------------------------------------------------------------------------------------
+template <typename T, int MT, bool GATHER>
+static void launch_w8a16_t(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
+                           int K, int w_rows, const int* rows, hipStream_t st) {
+    constexpr int NS = 3, LDS = 4 * NS * 16 * 128;
+    w8a16_kernel<T, MT, NS, GATHER><<<(N + 15) / 16, 256, LDS, st>>>(
+        static_cast<const uint16_t*>(x), static_cast<const int8_t*>(w), static_cast<const float*>(s),
+        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), M, N, K, w_rows, rows);
+}
+template <typename T>
+static void launch_w8a16(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
+                         int w_rows, const int* rows, hipStream_t st) {
+    if (M <= 16) {
+        if (rows) launch_w8a16_t<T, 1, true>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
+        else launch_w8a16_t<T, 1, false>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
+    } else {
+        if (rows) launch_w8a16_t<T, 2, true>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
+        else launch_w8a16_t<T, 2, false>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
+    }
+}
+
+static int w8a16_entry(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
+                       int dtype, int w_rows, const int* rows, void* stream) {
+    if (M < 1 || M > 32 || N < 1 || K < 16 || (K & 15) != 0 || w_rows < 1 || (long)w_rows * K >= (1L << 31)) return -1;
+    if (dtype != DT_F16 && dtype != DT_BF16) return -1;
+    if (!x || !w || !s || !out || (uintptr_t)x % 16 != 0 || (uintptr_t)w % 16 != 0) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == DT_F16) launch_w8a16<f16>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
+    else launch_w8a16<bf16>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
+    return (int)hipGetLastError();
+}
+
+// The int8 LM head (csrc/w8a16_gemv.cu:145-154, same arguments; M <= 32 here, against 16 there): out [M, N] of x [M, K]
+// fp16 / bf16 (dtype 0 / 1) times the int8 rows w [N, K] with float32 per-row scales s [N] and an optional bias [N]
+// of the activation type.  Returns -1 on bad arguments (M outside 1..32, K % 16, alignment), else the launch error.
+extern "C" int w8a16_gemv(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
+                          int dtype, void* stream) {
+    return w8a16_entry(x, w, s, bias, out, M, N, K, dtype, N, nullptr, stream);
+}
+
+// The same over a gathered subset of weight rows (csrc/w8a16_gemv.cu:145-146,156-167): rows int32 [N] indexes the
+// w_rows rows of w; out [M, N] is compact over the subset.  w_rows (the row count of w, which bounds the loads) is an
+// argument the reference does not need.
+extern "C" int w8a16_gemv_rows(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
+                               int K, int dtype, const void* rows, int w_rows, void* stream) {
+    if (!rows) return -1;
+    return w8a16_entry(x, w, s, bias, out, M, N, K, dtype, w_rows, static_cast<const int*>(rows), stream);
 }
