@@ -12,6 +12,7 @@ Also reported:
   gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline);
   quant: per-token quant at M=4096, K=5120, SiLU*up+quant at M=4096, I=17408, and the AR8 all-reduce operand
     (quantize; dequantised sum of 2 and 8 ranks) at 4096 x 5120, in GB/s (HBM-bound);
+  lm_head_w8a16: the int8 LM head (W8A16) over a 248,320 x 5120 vocabulary at M = 1, 4, 16, GB/s (HBM-bound);
   cpu_baseline: the reference's CPU path restated (oracle/cpu_path.py: torch CPU int8 matmul + dequant), timed on a
     bounded sample on this host's cores;
   mlp_chain: the fused MLP tail at M=4096 as the reference runs it (residual add + RMSNorm + int8 quant -> gate_up
@@ -410,6 +411,25 @@ def bench_headline(torch, L, st, dev, args):
     del a8, p8, o8
     print(f"[bench] AR8 n={n8}: {ar8_res}", file=sys.stderr, flush=True)
 
+    # int8 LM head (W8A16) over the 27B model's 248,320-row vocabulary at K = 5120, bf16 logits, M = 1 / 4 / 16
+    Nh = 248320
+    wh = torch.randint(-127, 128, (Nh, Kg), dtype=torch.int8, device=dev)
+    sh = torch.rand(Nh, device=dev) * 1e-3
+    head = {}
+    for Mh in (1, 4, 16):
+        xh = torch.randn(Mh, Kg, device=dev).to(torch.bfloat16)
+        oh = torch.empty(Mh, Nh, dtype=torch.bfloat16, device=dev)
+
+        def lmh(i, Mh=Mh, xh=xh, oh=oh):
+            if L.w8a16_gemv(xh.data_ptr(), wh.data_ptr(), sh.data_ptr(), None, oh.data_ptr(), Mh, Nh, Kg, 1, st()) != 0:
+                raise RuntimeError("w8a16_gemv")
+        ms_h, _ = graph_time(torch, lmh, 4, 40, 8)
+        b_h = Nh * Kg + 4 * Nh + 2 * Mh * Kg + 2 * Mh * Nh
+        head[f"M{Mh}"] = {"us": round(ms_h * 1e3, 2), "gbs": round(b_h / ms_h / 1e6, 1),
+                          "frac": round(b_h / ms_h / 1e6 / HBM_PEAK_GBS, 4)}
+    del wh, sh
+    print(f"[bench] int8 LM head N={Nh} K={Kg}: {head}", file=sys.stderr, flush=True)
+
     # ---- CPU baseline: the reference's CPU path (torch int8 matmul + dequant), bounded sample ---------------------
     cpu = None
     cpu_gemm = None
@@ -460,6 +480,7 @@ def bench_headline(torch, L, st, dev, args):
                   "silu_mul_quant_M4096_I17408": {"us": round(ms_s * 1e3, 2),
                                                    "gbs": round(smq_bytes / (ms_s * 1e-3) / 1e9, 1)},
                   "ar8_n20971520": ar8_res},
+        "lm_head_w8a16": {"workload": f"int8 LM head N={Nh} K={Kg}, bf16 activations and logits", **head},
     }
     return result
 
