@@ -398,8 +398,10 @@ GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80
 
 
 # prefill kernel as dispatched (1), its small configuration alone (3) and its main configuration alone (4); the
-# 320- and 384-super-tile shapes take the split launch (main for the whole rounds over the CUs, small for the rest)
-GEMM_SPLIT_SHAPES = [(4096, 5120, 256), (2048, 12288, 128), (4160, 5136, 144)]
+# 320- and 384-super-tile shapes take the split launch (main for the whole rounds over the CUs, small for the rest);
+# the 1536- and 1649-super-tile shapes take the long-grid variant of the main configuration (next-stage loads placed
+# differently), the second with a small-configuration remainder and a ragged K of three stages
+GEMM_SPLIT_SHAPES = [(4096, 5120, 256), (2048, 12288, 128), (4160, 5136, 144), (4096, 24576, 144), (4160, 24592, 272)]
 
 
 @pytest.mark.parametrize("kernel", [1, 3, 4])

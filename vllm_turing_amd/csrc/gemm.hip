@@ -312,23 +312,30 @@ typedef __attribute__((address_space(3))) void lds_void;
 // logical chunk ch[j] of its row at offset o*[j]; chunks past the end of K get an offset outside the buffer, which
 // makes the load write zeros.  A plain device function (bpw is a constant after inlining): in a template context the
 // host pass treats the buffer-descriptor type as a substitution failure and silently drops the kernel's host stub.
-__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rsa, __amdgpu_buffer_rsrc_t rsw, uint8_t* stage_l,
-                                          int a_bytes, const int* oa, const int* ow, const int* ch, int bpw, int k0,
-                                          int K, int wave) {
+__device__ __forceinline__ void dma_part(__amdgpu_buffer_rsrc_t rsa, __amdgpu_buffer_rsrc_t rsw, uint8_t* stage_l,
+                                         int a_bytes, const int* oa, const int* ow, const int* ch, int bpw, int j0,
+                                         int j1, int k0, int K, int wave) {
     uint8_t* sa_l = stage_l;
     uint8_t* sw_l = stage_l + a_bytes;
 #pragma unroll
-    for (int j = 0; j < bpw; ++j) {
+    for (int j = j0; j < j1; ++j) {
         const int blk = (wave * bpw + j) * 1024;
         const bool ok = k0 + ch[j] * 16 < K;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sa_l + blk), 16, ok ? oa[j] : 0x7fffffff, k0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sw_l + blk), 16, ok ? ow[j] : 0x7fffffff, k0, 0, 0);
     }
 }
+__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rsa, __amdgpu_buffer_rsrc_t rsw, uint8_t* stage_l,
+                                          int a_bytes, const int* oa, const int* ow, const int* ch, int bpw, int k0,
+                                          int K, int wave) {
+    dma_part(rsa, rsw, stage_l, a_bytes, oa, ow, ch, bpw, 0, bpw, k0, K, wave);
+}
+
 
 // WM x WN wavefronts (main configuration 2 x 4: two per SIMD, so one wavefront's LDS and barrier waits are covered by
 // the other's MFMAs).  Workgroup u of the grid computes quarter (or whole) tile u % SUB of super tile t_base + u / SUB.
-template <typename T, int EPI, int WM, int WN, int FM, int FN, int KB, int NS, int GM = GROUP_M, bool PRIO = false>
+template <typename T, int EPI, int WM, int WN, int FM, int FN, int KB, int NS, int SPLIT = 0, bool LEAD = false,
+          int GM = GROUP_M, bool PRIO = false>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                             const float* __restrict__ sa, const float* __restrict__ sw,
                                                             const uint16_t* __restrict__ bias, void* __restrict__ out,
@@ -372,6 +379,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
     auto issue = [&](int stage, int k0) {
         dma_stage(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, ow, ch, BPW, k0, K, wave);
     };
+    auto issue_part = [&](int stage, int k0, int j0, int j1) {
+        dma_part(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, ow, ch, BPW, j0, j1, k0, K, wave);
+    };
+    static_assert(SPLIT == 0 || (BPW % SPLIT == 0 && SPLIT <= KB / 32 + (LEAD ? 1 : 0)), "DMA slices");
 
     const int wm = wave / WN, wn = wave % WN;
     v16i acc[FM][FN];
@@ -382,7 +393,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-    auto compute = [&](int stage) {
+    auto compute = [&](int stage, int nstage, int nk0) {    // nk0 < 0: no next stage to load
         const v4i* la = reinterpret_cast<const v4i*>(lbase + stage * Cfg::STAGE_BYTES);
         const v4i* lw = la + BM * CPR;
         v4i fa[2][FM], fw[2][FN];
@@ -409,13 +420,19 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);   // favour the wavefront issuing MFMAs (measured neutral)
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM; ++i) {
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub & 1][j], fa[sub & 1][i], acc[i][j], 0, 0,
                                                                       0);
+            }
             if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (SPLIT > 0) {                       // next-stage slice sl after this sub-step's MFMAs
+                const int sl = sub + (LEAD ? 1 : 0);
+                if (sl < SPLIT && nk0 >= 0) issue_part(nstage, nk0, sl * BPW / SPLIT, (sl + 1) * BPW / SPLIT);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
 
@@ -433,8 +450,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
         // every wavefront's part of stage kt is in LDS (each waited for its own loads above).  A bare s_barrier:
         // __syncthreads() would also wait for the loads of the later stages still in flight.
         __builtin_amdgcn_s_barrier();
-        if (kt + NS - 1 < nk) issue((kt + NS - 1) % NS, (kt + NS - 1) * KB);
-        compute(kt % NS);
+        const bool more = kt + NS - 1 < nk;
+        if (SPLIT == 0 && more) issue((kt + NS - 1) % NS, (kt + NS - 1) * KB);
+        if (SPLIT > 0 && LEAD && more) issue_part((kt + NS - 1) % NS, (kt + NS - 1) * KB, 0, BPW / SPLIT);
+        compute(kt % NS, (kt + NS - 1) % NS, more ? (kt + NS - 1) * KB : -1);
     }
 
     // D fragment of v_mfma_i32_32x32x32_i8 with the weights as the A operand: lane holds column lane % 32 of the
@@ -773,8 +792,25 @@ static void launch_stream(const Args& p) {
 // ~9% faster than 64-byte stages x 4 at every prefill shape (half the barriers outweigh the shorter prefetch distance).
 // Small configuration: 128 x 128 quarter tiles, 2 x 2 wavefronts of 64 x 64, the same stages (64 KB: two workgroups
 // per CU).
-struct MainCfg { static constexpr int WM = 2, WN = 4, FM = 4, FN = 2, KB = 128, NS = 2; };
-struct SmallCfg { static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128, NS = 2; };
+// Where the next stage's loads are issued (SPLIT slices; LEAD: the first at the barrier): the main configuration issues
+// its two slices after the MFMAs of sub-steps 0 and 1 rather than in one burst after the barrier, where the issue
+// blocked each wavefront for ~940 of the ~3300 cycles of a stage (s_memtime stamps at M = N = 4096: 253 -> 229 us at
+// M 4096 x N 12288 x K 5120).  Long grids (at least LONG_ROUNDS rounds of super tiles over the CUs) measured best
+// with the first slice at the barrier (720 -> 695 us at N = 34816; 741 us with the main placement); the small
+// configuration best with one burst.
+struct MainCfg {
+    static constexpr int WM = 2, WN = 4, FM = 4, FN = 2, KB = 128, NS = 2, SPLIT = 2;
+    static constexpr bool LEAD = false;
+};
+struct LongCfg {
+    static constexpr int WM = 2, WN = 4, FM = 4, FN = 2, KB = 128, NS = 2, SPLIT = 2;
+    static constexpr bool LEAD = true;
+};
+struct SmallCfg {
+    static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128, NS = 2, SPLIT = 0;
+    static constexpr bool LEAD = false;
+};
+constexpr int LONG_ROUNDS = 6;
 
 // Which configuration covers which super tiles: 0 = main only, 2 = small only, 1 = main for the whole rounds of super
 // tiles over the CUs and small for a last partial round of at most CUs / W8_SMALL_REM_DIV super tiles.
@@ -788,10 +824,11 @@ struct SmallCfg { static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128,
 template <typename T, int EPI, typename C>
 static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
     using G = GemmCfg<C::WM, C::WN, C::FM, C::FN, C::KB, C::NS>;
-    const void* kern = reinterpret_cast<const void*>(&gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS>);
+    const void* kern = reinterpret_cast<const void*>(
+        &gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD>);
     static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
     (void)attr;
-    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
+    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
         p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
 }
 
@@ -818,11 +855,14 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
     }
     const int cus = cu_count();
     const int full = tiles / cus * cus, rem = tiles - full;
+    const bool longk = tiles >= LONG_ROUNDS * cus;
     if (policy == 0 || rem == 0 || rem > cus / W8_SMALL_REM_DIV) {
-        launch_gemm_cfg<T, EPI, MainCfg>(p, 0, tiles);
+        if (longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, tiles);
+        else launch_gemm_cfg<T, EPI, MainCfg>(p, 0, tiles);
         return;
     }
-    if (full > 0) launch_gemm_cfg<T, EPI, MainCfg>(p, 0, full);
+    if (full > 0 && longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, full);
+    else if (full > 0) launch_gemm_cfg<T, EPI, MainCfg>(p, 0, full);
     launch_gemm_cfg<T, EPI, SmallCfg>(p, full, rem * SUB);
 }
 
