@@ -297,7 +297,10 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
         const uint2 hi = *reinterpret_cast<const uint2*>(eb + rl * PITCH + cl * 2 + 8);
         if (m >= M) continue;
         if (vec && n + 7 < N) {
-            *reinterpret_cast<uint4*>(o + (long)m * N + n) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            // streaming (non-temporal) store: every workgroup of a round writes its tile at the same time, and the
+            // burst drains faster without allocating the lines in L2 (C3 253 -> 244 us, N = 34816 726 -> 695 us)
+            const v4i v = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(o + (long)m * N + n));
         } else {
             const uint32_t wds[4] = {lo.x, lo.y, hi.x, hi.y};
             for (int e = 0; e < 8 && n + e < N; ++e)
