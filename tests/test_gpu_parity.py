@@ -328,7 +328,11 @@ def test_per_token_quant_abi_errors(L):
 # SiLU * up + quant
 # ---------------------------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,I", [(1, 8704), (7, 8704), (1680, 8704), (300, 4096), (5, 136), (4, 17408), (2, 65536)])
+# M >= 512 and I <= 40960 take the table kernel (one persistent block per CU): (1680, 8704), (4096, 17408),
+# (600, 136), (513, 8), (520, 40960); (520, 65536) the direct kernel
+@pytest.mark.parametrize("M,I", [(1, 8704), (7, 8704), (1680, 8704), (300, 4096), (5, 136), (4, 17408), (2, 65536),
+                                 (4096, 17408), (520, 65536), (600, 136), (513, 8),
+                                 (520, 40960)])
 def test_silu_mul_quant(L, dt, M, I):
     say(f"silu_mul_quant M={M} I={I} {dt}")
     from vllm_turing_amd import silu_mul_quant
@@ -340,6 +344,29 @@ def test_silu_mul_quant(L, dt, M, I):
     qr, sr, _ = oracle.silu_mul_quant(gu)
     assert np.array_equal(q.cpu().numpy(), qr), int((q.cpu().numpy() != qr).sum())
     assert np.array_equal(s.cpu().view(-1).numpy(), sr)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_silu_mul_quant_table_exhaustive(L, dt):
+    """Every 16-bit gate pattern (NaN and infinity included) through the table kernel (512 rows of 128) against the
+    direct kernel (the same rows in launches of 64): bit-identical q and scales."""
+    say(f"silu table kernel exhaustive {dt}")
+    g = torch.Generator().manual_seed(5)
+    pat = torch.arange(65536, dtype=torch.int32)
+    gate = torch.where(pat >= 32768, pat - 65536, pat).to(torch.int16).view(dt).view(512, 128)
+    up = (torch.randn(512, 128, generator=g) * 2).to(dt)
+    gu = torch.cat([gate, up], dim=1).contiguous().to(DEV)
+    fn = L.silu_mul_quant if dt == torch.float16 else L.silu_mul_quant_bf16
+    q_t = torch.empty(512, 128, dtype=torch.int8, device=DEV)
+    s_t = torch.empty(512, dtype=torch.float32, device=DEV)
+    assert fn(gu.data_ptr(), q_t.data_ptr(), s_t.data_ptr(), 512, 128, stream()) == 0
+    q_d = torch.empty_like(q_t)
+    s_d = torch.empty_like(s_t)
+    for r0 in range(0, 512, 64):
+        assert fn(gu[r0:].data_ptr(), q_d[r0:].data_ptr(), s_d[r0:].data_ptr(), 64, 128, stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(q_t, q_d), int((q_t != q_d).sum())
+    assert torch.equal(s_t.view(torch.int32), s_d.view(torch.int32))
 
 
 def test_silu_mul_quant_codes(L):

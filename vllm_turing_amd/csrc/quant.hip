@@ -21,6 +21,10 @@
 // ~1e-12), y = RN_T(float(RN_T(s * rms)) * w), scale = max(absmax(y) / 127, FLT_EPSILON), q = rint(y * (1 / scale)).
 #include <float.h>
 
+#include <atomic>
+#include <mutex>
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/w8a8_mi355.h"
 
@@ -164,6 +168,110 @@ template <typename T>
 __global__ void silu_table_kernel(uint16_t* __restrict__ out) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < 65536) out[i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
+}
+
+// ---- SiLU * up + quant through a table of the 16-bit silu --------------------------------------------------------
+// silu is rounded to 16 bits before the product, so it is a function of the 16-bit gate pattern alone: the device
+// computes its value for all 65,536 patterns once (silu_lut_init_kernel: the same silu_f and rounding as the kernel
+// above, so the table kernel is bit-identical to it by construction), and a persistent block per CU copies the
+// 128 KB table of its dtype into LDS and looks the gate up.  ~12 VALU instructions per element instead of ~42, which
+// takes the kernel from VALU-bound to HBM-bound at prefill sizes.
+__device__ uint16_t g_silu_lut[2][65536];
+
+template <typename T>
+__global__ void __launch_bounds__(256) silu_lut_init_kernel() {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 65536) g_silu_lut[std::is_same<T, bf16>::value ? DT_BF16 : DT_F16][i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
+}
+
+constexpr int LUT_ENTRIES = 65536;
+constexpr int LUT_LDS_BYTES = LUT_ENTRIES * 2 + 2 * 16 * 4;   // the table, then two reduction buffers
+
+template <typename T>
+__device__ __forceinline__ uint32_t silu_mul_lut2(const uint16_t* lut, uint32_t g2, uint32_t u2, float& amax) {
+    const uint16_t lo = from_float<T>(to_float(T{lut[g2 & 0xffff]}) * lo_half(u2, T{}));
+    const uint16_t hi = from_float<T>(to_float(T{lut[g2 >> 16]}) * hi_half(u2, T{}));
+    const uint32_t o = (uint32_t)lo | ((uint32_t)hi << 16);
+    amax = __builtin_fmaxf(amax, __builtin_fabsf(lo_half(o, T{})));
+    amax = __builtin_fmaxf(amax, __builtin_fabsf(hi_half(o, T{})));
+    return o;
+}
+
+// Block b takes rows b, b + gridDim.x, ...; the next row's gate and up vectors are loaded (into the other register
+// buffer) before the current row is computed, so the loads overlap its table lookups, reduction and stores.
+template <typename T, int VPT>
+__global__ void __launch_bounds__(1024) silu_mul_quant_lut_kernel(const uint16_t* __restrict__ gu,
+                                                                  int8_t* __restrict__ q, float* __restrict__ scales,
+                                                                  int M, int I) {
+    extern __shared__ uint4 lds_lut[];
+    uint16_t* lut = reinterpret_cast<uint16_t*>(lds_lut);
+    float* red = reinterpret_cast<float*>(lut + LUT_ENTRIES);
+    const uint4* src = reinterpret_cast<const uint4*>(g_silu_lut[std::is_same<T, bf16>::value ? DT_BF16 : DT_F16]);
+    for (int i = threadIdx.x; i < LUT_ENTRIES / 8; i += blockDim.x) lds_lut[i] = src[i];
+
+    const int nvec = I >> 3;
+    uint4 gv[2][VPT], uv[2][VPT];
+    auto load = [&](int b, long row) {
+        const uint4* g4 = reinterpret_cast<const uint4*>(gu + row * 2 * (long)I);
+        const uint4* u4 = reinterpret_cast<const uint4*>(gu + row * 2 * (long)I + I);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int idx = threadIdx.x + j * blockDim.x;
+            if (idx < nvec) {
+                gv[b][j] = g4[idx];
+                uv[b][j] = u4[idx];
+            }
+        }
+    };
+    // alternate reduction buffers (by buffer b): a thread still reading one row's buffer is never overwritten by the
+    // next row, whose writes come after the next barrier
+    auto process = [&](int b, long row) {
+        uint4 r[VPT];
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int idx = threadIdx.x + j * blockDim.x;
+            r[j] = make_uint4(0, 0, 0, 0);
+            if (idx < nvec) {
+                r[j].x = silu_mul_lut2<T>(lut, gv[b][j].x, uv[b][j].x, amax);
+                r[j].y = silu_mul_lut2<T>(lut, gv[b][j].y, uv[b][j].y, amax);
+                r[j].z = silu_mul_lut2<T>(lut, gv[b][j].z, uv[b][j].z, amax);
+                r[j].w = silu_mul_lut2<T>(lut, gv[b][j].w, uv[b][j].w, amax);
+            }
+        }
+        amax = block_max(amax, red + 16 * b);
+        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+        if (threadIdx.x == 0) scales[row] = amax / 127.0f;
+        uint2* qo = reinterpret_cast<uint2*>(q + row * (long)I);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int idx = threadIdx.x + j * blockDim.x;
+            if (idx < nvec) {
+                const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+                int bq[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    bq[2 * e] = q8(lo_half(w[e], T{}) * inv);
+                    bq[2 * e + 1] = q8(hi_half(w[e], T{}) * inv);
+                }
+                qo[idx] = make_uint2(pack4(bq[0], bq[1], bq[2], bq[3]), pack4(bq[4], bq[5], bq[6], bq[7]));
+            }
+        }
+    };
+    const long G = gridDim.x;
+    long row = blockIdx.x;
+    load(0, row);
+    __syncthreads();                                      // the table is in LDS
+    while (true) {
+        if (row + G < M) load(1, row + G);
+        process(0, row);
+        row += G;
+        if (row >= M) break;
+        if (row + G < M) load(0, row + G);
+        process(1, row);
+        row += G;
+        if (row >= M) break;
+    }
 }
 
 // ---- residual add + RMSNorm + per-token quant ----------------------------------------------------------------------
@@ -364,8 +472,73 @@ static int run_ptq(const void* x, void* q, void* s, int M, int K, long ldx, hipS
     return 0;
 }
 
+// The silu tables are built on a device by the first call there that is not being captured into a graph, and
+// synchronised once, so that every stream of the device sees them; until then (and under capture) calls take the
+// direct kernel.
+constexpr int LUT_MIN_ROWS = 512;                         // measured: below it the direct kernel is as fast
+constexpr int LUT_MAX_VPT = 5;                            // I <= 40960: two row buffers in registers, no spills
+static std::atomic<int> g_lut_ready[64][2];
+static std::mutex g_lut_mu;
+
+static bool silu_lut_ready(int dt, hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (g_lut_ready[dev][dt].load(std::memory_order_acquire)) return true;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return false;
+    }
+    std::lock_guard<std::mutex> lock(g_lut_mu);
+    if (g_lut_ready[dev][dt].load(std::memory_order_acquire)) return true;
+    if (dt == DT_F16) silu_lut_init_kernel<f16><<<LUT_ENTRIES / 256, 256, 0, st>>>();
+    else silu_lut_init_kernel<bf16><<<LUT_ENTRIES / 256, 256, 0, st>>>();
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    g_lut_ready[dev][dt].store(1, std::memory_order_release);
+    return true;
+}
+
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev] = v;
+    }
+    return cached[dev];
+}
+
+template <typename T, int VPT>
+static void launch_smq_lut(const uint16_t* gp, int8_t* qp, float* sp, int M, int I, int threads, hipStream_t st) {
+    const void* kern = reinterpret_cast<const void*>(&silu_mul_quant_lut_kernel<T, VPT>);
+    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, LUT_LDS_BYTES);
+    (void)attr;
+    const int grid = M < device_cus() ? M : device_cus();
+    silu_mul_quant_lut_kernel<T, VPT><<<grid, threads, LUT_LDS_BYTES, st>>>(gp, qp, sp, M, I);
+}
+
 template <typename T>
 static int run_smq(const void* gu, void* q, void* s, int M, int I, hipStream_t st) {
+    const int nvec = I / 8, lvpt = (nvec + 1023) / 1024;
+    if (M >= LUT_MIN_ROWS && lvpt <= LUT_MAX_VPT &&
+        silu_lut_ready(std::is_same<T, bf16>::value ? DT_BF16 : DT_F16, st)) {
+        const int threads = ((nvec + lvpt - 1) / lvpt + 63) / 64 * 64;
+        const uint16_t* gp = static_cast<const uint16_t*>(gu);
+        int8_t* qp = static_cast<int8_t*>(q);
+        float* sp = static_cast<float*>(s);
+        switch (lvpt) {
+#define W8_CASE(V) case V: launch_smq_lut<T, V>(gp, qp, sp, M, I, threads, st); break;
+            W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5)
+#undef W8_CASE
+            default: return 1;
+        }
+        return 0;
+    }
     int vpt = 0;
     const int threads = pick_threads(I / 8, MAX_VPT_SILU, &vpt);
     if (vpt > MAX_VPT_SILU) return 1;
