@@ -73,7 +73,7 @@ __device__ __forceinline__ v4i wload(const int8_t* p) {
 // registers for the whole kernel.  Rows are grid-strided over the wavefronts, R rows per iteration with the next
 // iteration's loads issued before this one's v_dot4 math (double buffering).  Each row's per-lane partial sums are
 // reduced across the wavefront with DPP row operations, ds_swizzle and readlane.
-template <typename T, int M, int CH, int R, int EPI, bool NT = false>
+template <typename T, int M, int CH, int R, int EPI, bool NT = true>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
                                                         const uint16_t* __restrict__ bias, void* __restrict__ out,
@@ -310,6 +310,7 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+constexpr int CPOL_NT = 2;                                // cache-policy operand of a buffer load: non-temporal
 
 // One K stage of a wavefront's share of A and W (bpw 1 KB blocks of each), straight into LDS.  Block j's lane reads
 // logical chunk ch[j] of its row at offset o*[j]; chunks past the end of K get an offset outside the buffer, which
@@ -485,8 +486,12 @@ __device__ __forceinline__ void dma_step(__amdgpu_buffer_rsrc_t rsw, __amdgpu_bu
 #pragma unroll
     for (int j = 0; j < lps; ++j) {
         const bool ok = k0 + chk[j] * 16 < K;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(j < 2 ? rsw : rsa, (lds_void*)(dst + j * 1024), 16,
-                                                 ok ? off[j] : 0x7fffffff, k0, 0, 0);
+        if (j < 2)                                       // weights, read once: non-temporal
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(dst + j * 1024), 16, ok ? off[j] : 0x7fffffff,
+                                                     k0, 0, CPOL_NT);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(dst + j * 1024), 16, ok ? off[j] : 0x7fffffff,
+                                                     k0, 0, 0);
     }
 }
 
@@ -714,6 +719,19 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
 // ---------------------------------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------------------------------
+// Compute units of the current device (cached per device).
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev] = v;
+    }
+    return cached[dev];
+}
+
 struct Args {
     const int8_t* a;
     const int8_t* w;
@@ -725,11 +743,10 @@ struct Args {
     hipStream_t st;
 };
 
-// One or two activation rows: the VALU kernel, one wavefront per two weight rows (measured fastest for K = 5120,
-// N = 17408: 16.8 us against 18.1 for the LDS-ring MFMA kernel; every wavefront issues its loads at once and the
-// whole grid is resident), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two rows up to K = 8192 (past
-// that the LDS-ring kernel wins, 19.6 vs 22.0 us at K = 17408).  Chunk counts are rounded up to the next of 1..8, 10,
-// 12, 14, 17 (chunks past K are masked).
+// One or two activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
+// vs 18.1 us at K = 5120, N = 17408), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two rows up to
+// K = 8192 (past that the LDS-ring kernel won, 19.6 vs 22.0 us at K = 17408).  Chunk counts are rounded up to the
+// next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
 constexpr int DOT4_MAX_M = 2, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8;
 
 static int dot4_chunks(int K) {
@@ -737,12 +754,25 @@ static int dot4_chunks(int K) {
     return c <= 8 ? c : c <= 10 ? 10 : c <= 12 ? 12 : c <= 14 ? 14 : c <= 17 ? 17 : 1 << 20;
 }
 
+// Grid: at most DOT4_BLOCKS_PER_CU workgroups per CU that are resident together (fewer when the registers of a long K
+// allow fewer), the same number on every CU, rows grid-strided over their wavefronts.  At K = 5120, N = 17408 with
+// non-temporal weight loads: M=1 16.9 -> 15.1 us, M=2 19.3 -> 15.8 us against one wavefront per two rows with
+// ordinary loads (the non-temporal loads alone: 15.1 and 17.6 us).
+constexpr int DOT4_BLOCKS_PER_CU = 4;
+
 template <typename T, int M, int CH, int EPI>
 static void launch_dot4_ch(const Args& p) {
     if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2)) {
-        const int waves = (p.N + 1) / 2;
-        gemv_dot4_kernel<T, M, CH, 1, EPI><<<(waves + 3) / 4, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
-                                                                                p.N, p.K, p.sa_rows, p.sw_rows);
+        const void* kern = reinterpret_cast<const void*>(&gemv_dot4_kernel<T, M, CH, 1, EPI>);
+        static const int occ = [kern] {
+            int nb = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
+            return nb;
+        }();
+        const int per_cu = occ < DOT4_BLOCKS_PER_CU ? occ : DOT4_BLOCKS_PER_CU;
+        const int need = (p.N + 3) / 4, full = cu_count() * per_cu;
+        gemv_dot4_kernel<T, M, CH, 1, EPI><<<need < full ? need : full, 256, 0, p.st>>>(
+            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
     }
 }
 template <typename T, int M, int EPI>
@@ -835,18 +865,6 @@ static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
         p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
 }
 
-// Compute units of the current device (cached per device).
-static int cu_count() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cached[dev] = v;
-    }
-    return cached[dev];
-}
 
 template <typename T, int EPI>
 static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
