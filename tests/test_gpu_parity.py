@@ -662,3 +662,55 @@ def test_mlp_chain_small(L):
     o_ref, _ = cpu_path.scaled_mm(torch.from_numpy(aq_r), c["w_down"], torch.from_numpy(as_r), c["sw_down"], None,
                                   torch.bfloat16, 1)
     assert torch.equal(out.cpu(), o_ref) and torch.equal(out2.cpu(), o_ref)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# HIP graph capture: the decode and prefill callers replay captured launches
+# ---------------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 4, 600])
+def test_graph_replay_mlp(L, M):
+    """norm + quant -> gate_up -> SiLU*up + quant -> down (bf16) captured in one HIP graph and replayed three rounds
+    over three inputs copied in eagerly, with eager work and synchronisations between replays: every replay equals the
+    eager run bit for bit (M = 600 takes the SiLU table kernel and the prefill GEMM, M = 1 and 4 the decode kernels)."""
+    say(f"graph replay MLP M={M}")
+    from vllm_turing_amd import cutlass_scaled_mm, rms_norm_dynamic_per_token_quant, silu_mul_quant
+    H, I = 1024, 2048
+    g = torch.Generator().manual_seed(M + 77)
+    wgu = torch.randint(-127, 128, (2 * I, H), dtype=torch.int8, generator=g).to(DEV)
+    sgu = (torch.rand(2 * I, 1, generator=g) * 1e-3 + 1e-4).to(DEV)
+    wd = torch.randint(-127, 128, (H, I), dtype=torch.int8, generator=g).to(DEV)
+    sd = (torch.rand(H, 1, generator=g) * 1e-3 + 1e-4).to(DEV)
+    nw = (1.0 + torch.randn(H, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    inputs = [torch.randn(M, H, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    x_in = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+
+    def step():
+        q, s = rms_norm_dynamic_per_token_quant(x_in, nw, 1e-6)
+        gu = cutlass_scaled_mm(q, wgu.t(), s, sgu, torch.bfloat16)
+        aq, a_s = silu_mul_quant(gu)
+        return cutlass_scaled_mm(aq, wd.t(), a_s, sd, torch.bfloat16)
+
+    refs = []
+    for xi in inputs:
+        x_in.copy_(xi)
+        refs.append(step().clone())
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        x_in.copy_(inputs[0])
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    torch.cuda.synchronize()
+    for rnd in range(3):
+        for k, (xi, ref) in enumerate(zip(inputs, refs)):
+            x_in.copy_(xi)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"round {rnd} input {k}: {int((out != ref).sum())} outputs differ"
+            assert float((x_in.float() * 2).abs().sum()) > 0       # eager work between replays
