@@ -7,7 +7,7 @@
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
 // Four kernels:
-//  * gemv_dot4_kernel, M = 1 and K <= 17408, or M = 2 and K <= 8192 (decode): weight-streaming through the VALU: each
+//  * gemv_dot4_kernel, M = 1 and K <= 17408, or M = 2, 3 and K <= 8192 (decode): weight-streaming through the VALU: each
 //    wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in
 //    registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
 //  * stream_lds_kernel, the rest of M <= 32 (decode, speculative verify): weight-streaming and HBM-bound.  A workgroup
@@ -743,11 +743,12 @@ struct Args {
     hipStream_t st;
 };
 
-// One or two activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
-// vs 18.1 us at K = 5120, N = 17408), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two rows up to
-// K = 8192 (past that the LDS-ring kernel won, 19.6 vs 22.0 us at K = 17408).  Chunk counts are rounded up to the
+// One to three activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
+// vs 18.1 us at K = 5120, N = 17408), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two or three rows
+// up to K = 8192 (past that the LDS-ring kernel won, 19.6 vs 22.0 us at K = 17408, M = 2).  Three rows: 17.4 vs
+// 18.4 us at K = 5120, N = 17408; four rows lose (20.2 vs 18.6: the activations' registers halve the occupancy).  Chunk counts are rounded up to the
 // next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
-constexpr int DOT4_MAX_M = 2, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8;
+constexpr int DOT4_MAX_M = 3, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8;
 
 static int dot4_chunks(int K) {
     const int c = (K / 16 + 63) / 64;
@@ -795,6 +796,7 @@ static void launch_dot4(const Args& p) {
     switch (p.M) {
         case 1: launch_dot4_m<T, 1, EPI>(p); break;
         case 2: launch_dot4_m<T, 2, EPI>(p); break;
+        case 3: launch_dot4_m<T, 3, EPI>(p); break;
     }
 }
 
