@@ -102,8 +102,10 @@ def _ulp16_t(v, dt):
     return 2.0 ** (e - mant)
 
 
+# M = 1 (K <= 8192) and M = 2 (K <= 5120) take the VALU kernel, the rest the MFMA kernel
 W8A16_CASES = [(1, 17408, 5120), (4, 4096, 5120), (16, 1000, 2048), (5, 333, 4112), (32, 2048, 1024), (17, 64, 16),
-               (3, 248320 // 8, 5120)]
+               (3, 248320 // 8, 5120), (2, 1000, 2048), (1, 7, 16), (1, 333, 8192), (2, 129, 5120), (1, 100, 8208),
+               (2, 31, 5136)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
@@ -135,6 +137,27 @@ def test_w8a16(L, dt, M, N, K):
     exact = (x.double() @ w.double().T) * s.double() + (bias.double() if bias is not None else 0)
     assert ((got - exact).abs() / (exact.abs() + 1e-3 * exact.abs().max())).max() < 1e-2 if dt == torch.bfloat16 \
         else ((got - exact).abs() / (exact.abs() + 1e-3 * exact.abs().max())).max() < 2e-3
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_w8a16_rows_small_m(L, M):
+    """Gathered rows (repeats, the first and last row) on the VALU kernel equal the dense logits' columns."""
+    say(f"w8a16 rows M={M}")
+    g = torch.Generator().manual_seed(11 + M)
+    N, K = 2500, 5120
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g).to(DEV)
+    sc = (torch.rand(N, generator=g) * 1e-3 + 1e-4).to(DEV)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV)
+    rows = torch.tensor([N - 1, 0, 5, 5, 1234, 77], dtype=torch.int32, device=DEV)
+    dense = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    sub = torch.empty(M, rows.numel(), dtype=torch.bfloat16, device=DEV)
+    assert L.w8a16_gemv(x.data_ptr(), w.data_ptr(), sc.data_ptr(), bias.data_ptr(), dense.data_ptr(), M, N, K, 1,
+                        stream()) == 0
+    assert L.w8a16_gemv_rows(x.data_ptr(), w.data_ptr(), sc.data_ptr(), bias.data_ptr(), sub.data_ptr(), M,
+                             rows.numel(), K, 1, rows.data_ptr(), N, stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(sub.cpu(), dense[:, rows.long()].cpu())
 
 
 def test_w8a16_rows_and_api(L):

@@ -993,6 +993,158 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
 // ---------------------------------------------------------------------------------------------------------------------
 // W8A16 (int8 LM head)
 // ---------------------------------------------------------------------------------------------------------------------
+// w8a16_dot_kernel: M <= 2 rows of the int8 LM head through the VALU.  The weight stream of gemv_dot4_kernel (each
+// wavefront instruction reads 1 KB of one weight row, non-temporally; lane l owns the 16-byte chunks l, l + 64, ...;
+// rows grid-strided over at most four resident workgroups per CU, the next row's loads issued before this row's math);
+// each lane widens its 16 weights to 16-bit pairs (fp16 by the exact bit trick, bf16 through float32) and
+// accumulates v_dot2_f32_{f16,bf16} against the activations it keeps in registers; a row's float32 partial sums meet
+// across the wavefront (DPP, ds_swizzle, readlane; every lane ends with the same sum).  Sum order: each lane's chain
+// over its chunks, then the wavefront tree.
+typedef __bf16 bh2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v += dpp_f<0xB1>(v);                               // lane ^ 1
+    v += dpp_f<0x4E>(v);                               // lane ^ 2
+    v += dpp_f<0x141>(v);                              // row_half_mirror: groups of 8
+    v += dpp_f<0x140>(v);                              // row_mirror: rows of 16
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));   // lane ^ 16
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+// one dword of 4 int8 weights -> the 16-bit pairs (elements 0, 1) and (2, 3), exactly
+__device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, f16) {
+    const uint32_t a = d ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    p0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) - bias);
+    p1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) - bias);
+}
+__device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, bf16) {
+    const float f0 = (float)(int8_t)(d & 0xff), f1 = (float)(int8_t)((d >> 8) & 0xff);
+    const float f2 = (float)(int8_t)((d >> 16) & 0xff), f3 = (float)(int8_t)(d >> 24);
+    p0 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    p1 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+}
+__device__ __forceinline__ float dot2(uint32_t w2, uint32_t x2, float acc, f16) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w2), __builtin_bit_cast(h2, x2), acc, false);
+}
+__device__ __forceinline__ float dot2(uint32_t w2, uint32_t x2, float acc, bf16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bh2, w2), __builtin_bit_cast(bh2, x2), acc, false);
+}
+
+template <typename T, int M, int CH, bool GATHER>
+__global__ void __launch_bounds__(256) w8a16_dot_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                        const float* __restrict__ s, const uint16_t* __restrict__ bias,
+                                                        uint16_t* __restrict__ out, int N, int K, int w_rows,
+                                                        const int* __restrict__ rows) {
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (blockDim.x >> 6);
+    const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int K16 = K >> 4;
+    const v4i z = {0, 0, 0, 0};
+    v4i xv[M][CH][2];                                    // 16 activations (32 bytes) per chunk and row
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int c = lane + 64 * j;
+            const v4i* src = reinterpret_cast<const v4i*>(x + (long)m * K + c * 16);
+            xv[m][j][0] = c < K16 ? src[0] : z;
+            xv[m][j][1] = c < K16 ? src[1] : z;
+        }
+    auto src_row = [&](int n) { return GATHER ? min(max(rows[n], 0), w_rows - 1) : n; };
+    v4i wb[2][CH];
+    auto load = [&](int buf, int n) {
+        const int8_t* row = w + (long)src_row(n) * K;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int c = lane + 64 * j;
+            wb[buf][j] = c < K16 ? wload<true>(row + c * 16) : z;
+        }
+    };
+    auto finish = [&](int buf, int n) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {              // weight dword e: elements 4 e .. 4 e + 3 of the chunk
+                uint32_t p0, p1;
+                widen4((uint32_t)wb[buf][j][e], p0, p1, T{});
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    acc[m] = dot2(p0, (uint32_t)xv[m][j][e >> 1][2 * (e & 1)], acc[m], T{});
+                    acc[m] = dot2(p1, (uint32_t)xv[m][j][e >> 1][2 * (e & 1) + 1], acc[m], T{});
+                }
+            }
+        const int sr = src_row(n);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float t = wave_sum_f(acc[m]);
+            if (lane == m) {
+                const float b = bias ? to_float(T{bias[sr]}) : 0.0f;
+                out[(long)m * N + n] = from_float<T>(__builtin_fmaf(t, s[sr], b));
+            }
+        }
+    };
+    int n0 = wid;
+    if (n0 >= N) return;
+    load(0, n0);
+    while (true) {
+        if (n0 + nw < N) load(1, n0 + nw);
+        finish(0, n0);
+        n0 += nw;
+        if (n0 >= N) break;
+        if (n0 + nw < N) load(0, n0 + nw);
+        finish(1, n0);
+        n0 += nw;
+        if (n0 >= N) break;
+    }
+}
+
+// M = 1 up to K = 8192 and M = 2 up to K = 5120 (the activations' registers) take the VALU kernel.
+constexpr int W8A16_DOT_MAX_CH_M1 = 8, W8A16_DOT_MAX_CH_M2 = 5;
+
+template <typename T, int M, int CH, bool GATHER>
+static void launch_w8a16_dot_t(const void* x, const void* w, const void* s, const void* bias, void* out, int N, int K,
+                               int w_rows, const int* rows, hipStream_t st) {
+    const void* kern = reinterpret_cast<const void*>(&w8a16_dot_kernel<T, M, CH, GATHER>);
+    static const int occ = [kern] {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
+        return nb;
+    }();
+    const int per_cu = occ < DOT4_BLOCKS_PER_CU ? occ : DOT4_BLOCKS_PER_CU;
+    const int need = (N + 3) / 4, full = cu_count() * per_cu;
+    w8a16_dot_kernel<T, M, CH, GATHER><<<need < full ? need : full, 256, 0, st>>>(
+        static_cast<const uint16_t*>(x), static_cast<const int8_t*>(w), static_cast<const float*>(s),
+        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), N, K, w_rows, rows);
+}
+template <typename T, int M, bool GATHER>
+static bool launch_w8a16_dot_m(const void* x, const void* w, const void* s, const void* bias, void* out, int N, int K,
+                               int w_rows, const int* rows, hipStream_t st) {
+    const int ch = (K / 16 + 63) / 64;
+    if (ch > (M == 1 ? W8A16_DOT_MAX_CH_M1 : W8A16_DOT_MAX_CH_M2)) return false;
+    switch (ch) {
+#define W8_CASE(C) case C: if constexpr (M == 1 || C <= W8A16_DOT_MAX_CH_M2) \
+            launch_w8a16_dot_t<T, M, C, GATHER>(x, w, s, bias, out, N, K, w_rows, rows, st); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8)
+#undef W8_CASE
+        default: return false;
+    }
+    return true;
+}
+template <typename T>
+static bool launch_w8a16_dot(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
+                             int K, int w_rows, const int* rows, hipStream_t st) {
+    if (M == 1) return rows ? launch_w8a16_dot_m<T, 1, true>(x, w, s, bias, out, N, K, w_rows, rows, st)
+                            : launch_w8a16_dot_m<T, 1, false>(x, w, s, bias, out, N, K, w_rows, rows, st);
+    if (M == 2) return rows ? launch_w8a16_dot_m<T, 2, true>(x, w, s, bias, out, N, K, w_rows, rows, st)
+                            : launch_w8a16_dot_m<T, 2, false>(x, w, s, bias, out, N, K, w_rows, rows, st);
+    return false;
+}
+
 template <typename T, int MT, bool GATHER>
 static void launch_w8a16_t(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
                            int K, int w_rows, const int* rows, hipStream_t st) {
@@ -1004,6 +1156,7 @@ static void launch_w8a16_t(const void* x, const void* w, const void* s, const vo
 template <typename T>
 static void launch_w8a16(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
                          int w_rows, const int* rows, hipStream_t st) {
+    if (launch_w8a16_dot<T>(x, w, s, bias, out, M, N, K, w_rows, rows, st)) return;
     if (M <= 16) {
         if (rows) launch_w8a16_t<T, 1, true>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
         else launch_w8a16_t<T, 1, false>(x, w, s, bias, out, M, N, K, w_rows, rows, st);
