@@ -73,6 +73,23 @@ __device__ __forceinline__ v4i wload(const int8_t* p) {
 // registers for the whole kernel.  Rows are grid-strided over the wavefronts, R rows per iteration with the next
 // iteration's loads issued before this one's v_dot4 math (double buffering).  Each row's per-lane partial sums are
 // reduced across the wavefront with DPP row operations, ds_swizzle and readlane.
+// A 16-bit zero in device memory: the bias operand of a row without bias, so that the bias load is unconditional.
+__device__ const uint16_t g_zero16 = 0;
+
+// The same with the scales and bias already in registers.
+template <typename T, int EPI>
+__device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sam, float swn, float bn) {
+    if constexpr (EPI == EPI_I32) {
+        static_cast<int*>(out)[idx] = acc;
+    } else {
+        float r;
+        if constexpr (EPI == EPI_SMALL) r = epi_small(acc, sam, swn, bn);
+        else if constexpr (EPI == EPI_LARGE) r = epi_large(acc, sam, swn);
+        else r = epi_large_bias(acc, sam, swn, bn);
+        static_cast<uint16_t*>(out)[idx] = from_float<T>(r);
+    }
+}
+
 template <typename T, int M, int CH, int R, int EPI, bool NT = true>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
@@ -91,7 +108,12 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
             const int c = lane + 64 * j;
             av[m][j] = c < K16 ? *reinterpret_cast<const v4i*>(a + (long)m * K + c * 16) : z;
         }
+    float sam[M];                                        // row scales (none are read for the int32 output)
+#pragma unroll
+    for (int m = 0; m < M; ++m) sam[m] = EPI == EPI_I32 ? 0.0f : sa[sa_rows ? m : 0];
     v4i wb[2][R][CH];
+    float swb[2][R];                                     // the rows' column scale and bias bits, loaded with the row
+    uint16_t bb[2][R];
     auto load = [&](int buf, int n0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -100,8 +122,15 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int c = lane + 64 * j;
-                wb[buf][r][j] = (c < K16 && n0 + r * nw < N) ? wload<NT>(row + c * 16) : z;
+                // no mask on loaded values: a select after the load would make the compiler wait for it right
+                // there, serialising the next row's loads with this row's math.  Chunks past K read an in-bounds
+                // chunk and meet zero activations; rows past N read row N - 1 and are not stored.
+                wb[buf][r][j] = wload<NT>(row + min(c, K16 - 1) * 16);
             }
+            // unconditional loads, converted only in finish: a conditional load or a conversion next to it would
+            // make the compiler wait for the next row's weights as well
+            swb[buf][r] = EPI == EPI_I32 ? 0.0f : sw[sw_rows ? n : 0];
+            bb[buf][r] = EPI == EPI_SMALL || EPI == EPI_LARGE_BIAS ? *(bias ? bias + n : &g_zero16) : 0;
         }
     };
     auto finish = [&](int buf, int n0) {
@@ -127,22 +156,29 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
             for (int m = 0; m < M; ++m) {
                 const int n = n0 + r * nw;
                 if (lane == r * M + m && n < N)
-                    store_out<T, EPI>(out, (long)m * N + n, acc[r][m], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
+                    store_pre<T, EPI>(out, (long)m * N + n, acc[r][m], sam[m], swb[buf][r], to_float(T{bb[buf][r]}));
             }
     };
+    // Row groups wid, wid + stride, ... (cnt of them), each computed while the next group's loads are in flight.  The
+    // loop is peeled so that no load sits under a condition: then the compiler's wait before a group's math counts
+    // the next group's loads as still outstanding instead of waiting for them too.
     const int stride = R * nw;
-    int n0 = wid;
-    if (n0 >= N) return;
-    load(0, n0);
-    while (true) {
-        if (n0 + stride < N) load(1, n0 + stride);
-        finish(0, n0);
-        n0 += stride;
-        if (n0 >= N) break;
-        if (n0 + stride < N) load(0, n0 + stride);
-        finish(1, n0);
-        n0 += stride;
-        if (n0 >= N) break;
+    if (wid >= N) return;
+    const int cnt = (N - 1 - wid) / stride + 1;
+    load(0, wid);
+    int k = 0;
+    for (; k + 2 < cnt; k += 2) {
+        load(1, wid + (k + 1) * stride);
+        finish(0, wid + k * stride);
+        load(0, wid + (k + 2) * stride);
+        finish(1, wid + (k + 1) * stride);
+    }
+    if (k + 1 < cnt) {
+        load(1, wid + (k + 1) * stride);
+        finish(0, wid + k * stride);
+        finish(1, wid + (k + 1) * stride);
+    } else {
+        finish(0, wid + k * stride);
     }
 }
 
@@ -716,6 +752,125 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
     }
 }
 
+// w8a16_dot_kernel: M <= 2 rows of the int8 LM head through the VALU.  The weight stream of gemv_dot4_kernel (each
+// wavefront instruction reads 1 KB of one weight row, non-temporally; lane l owns the 16-byte chunks l, l + 64, ...;
+// rows grid-strided over at most four resident workgroups per CU, the next row's loads issued before this row's math);
+// each lane widens its 16 weights to 16-bit pairs (fp16 by the exact bit trick, bf16 through float32) and
+// accumulates v_dot2_f32_{f16,bf16} against the activations it keeps in registers; a row's float32 partial sums meet
+// across the wavefront (DPP, ds_swizzle, readlane; every lane ends with the same sum).  Sum order: each lane's chain
+// over its chunks, then the wavefront tree.
+typedef __bf16 bh2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v += dpp_f<0xB1>(v);                               // lane ^ 1
+    v += dpp_f<0x4E>(v);                               // lane ^ 2
+    v += dpp_f<0x141>(v);                              // row_half_mirror: groups of 8
+    v += dpp_f<0x140>(v);                              // row_mirror: rows of 16
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));   // lane ^ 16
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+// one dword of 4 int8 weights -> the 16-bit pairs (elements 0, 1) and (2, 3), exactly
+__device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, f16) {
+    const uint32_t a = d ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    p0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) - bias);
+    p1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) - bias);
+}
+__device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, bf16) {
+    const float f0 = (float)(int8_t)(d & 0xff), f1 = (float)(int8_t)((d >> 8) & 0xff);
+    const float f2 = (float)(int8_t)((d >> 16) & 0xff), f3 = (float)(int8_t)(d >> 24);
+    p0 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    p1 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+}
+__device__ __forceinline__ float dot2(uint32_t w2, uint32_t x2, float acc, f16) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w2), __builtin_bit_cast(h2, x2), acc, false);
+}
+__device__ __forceinline__ float dot2(uint32_t w2, uint32_t x2, float acc, bf16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bh2, w2), __builtin_bit_cast(bh2, x2), acc, false);
+}
+
+template <typename T, int M, int CH, bool GATHER>
+__global__ void __launch_bounds__(256) w8a16_dot_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                        const float* __restrict__ s, const uint16_t* __restrict__ bias,
+                                                        uint16_t* __restrict__ out, int N, int K, int w_rows,
+                                                        const int* __restrict__ rows) {
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (blockDim.x >> 6);
+    const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int K16 = K >> 4;
+    const v4i z = {0, 0, 0, 0};
+    v4i xv[M][CH][2];                                    // 16 activations (32 bytes) per chunk and row
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int c = lane + 64 * j;
+            const v4i* src = reinterpret_cast<const v4i*>(x + (long)m * K + c * 16);
+            xv[m][j][0] = c < K16 ? src[0] : z;
+            xv[m][j][1] = c < K16 ? src[1] : z;
+        }
+    auto src_row = [&](int n) { return GATHER ? min(max(rows[n], 0), w_rows - 1) : n; };
+    v4i wb[2][CH];
+    float sb[2];                                         // the row's scale and bias bits, loaded with the row
+    uint16_t bb[2];
+    auto load = [&](int buf, int n) {
+        const int sr = src_row(n);
+        const int8_t* row = w + (long)sr * K;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int c = lane + 64 * j;
+            wb[buf][j] = wload<true>(row + min(c, K16 - 1) * 16);   // unmasked (see gemv_dot4_kernel)
+        }
+        sb[buf] = s[sr];
+        bb[buf] = *(bias ? bias + sr : &g_zero16);       // unconditional (see gemv_dot4_kernel)
+    };
+    auto finish = [&](int buf, int n) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {              // weight dword e: elements 4 e .. 4 e + 3 of the chunk
+                uint32_t p0, p1;
+                widen4((uint32_t)wb[buf][j][e], p0, p1, T{});
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    acc[m] = dot2(p0, (uint32_t)xv[m][j][e >> 1][2 * (e & 1)], acc[m], T{});
+                    acc[m] = dot2(p1, (uint32_t)xv[m][j][e >> 1][2 * (e & 1) + 1], acc[m], T{});
+                }
+            }
+            // one chunk at a time: left free, the scheduler widens every chunk up front (bf16: 156 registers)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float t = wave_sum_f(acc[m]);
+            if (lane == m) out[(long)m * N + n] = from_float<T>(__builtin_fmaf(t, sb[buf], to_float(T{bb[buf]})));
+        }
+    };
+    // rows wid, wid + nw, ...: peeled as in gemv_dot4_kernel so that no load sits under a condition
+    if (wid >= N) return;
+    const int cnt = (N - 1 - wid) / nw + 1;
+    load(0, wid);
+    int k = 0;
+    for (; k + 2 < cnt; k += 2) {
+        load(1, wid + (k + 1) * nw);
+        finish(0, wid + k * nw);
+        load(0, wid + (k + 2) * nw);
+        finish(1, wid + (k + 1) * nw);
+    }
+    if (k + 1 < cnt) {
+        load(1, wid + (k + 1) * nw);
+        finish(0, wid + k * nw);
+        finish(1, wid + (k + 1) * nw);
+    } else {
+        finish(0, wid + k * nw);
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------------------------------
@@ -993,116 +1148,6 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
 // ---------------------------------------------------------------------------------------------------------------------
 // W8A16 (int8 LM head)
 // ---------------------------------------------------------------------------------------------------------------------
-// w8a16_dot_kernel: M <= 2 rows of the int8 LM head through the VALU.  The weight stream of gemv_dot4_kernel (each
-// wavefront instruction reads 1 KB of one weight row, non-temporally; lane l owns the 16-byte chunks l, l + 64, ...;
-// rows grid-strided over at most four resident workgroups per CU, the next row's loads issued before this row's math);
-// each lane widens its 16 weights to 16-bit pairs (fp16 by the exact bit trick, bf16 through float32) and
-// accumulates v_dot2_f32_{f16,bf16} against the activations it keeps in registers; a row's float32 partial sums meet
-// across the wavefront (DPP, ds_swizzle, readlane; every lane ends with the same sum).  Sum order: each lane's chain
-// over its chunks, then the wavefront tree.
-typedef __bf16 bh2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float wave_sum_f(float v) {
-    v += dpp_f<0xB1>(v);                               // lane ^ 1
-    v += dpp_f<0x4E>(v);                               // lane ^ 2
-    v += dpp_f<0x141>(v);                              // row_half_mirror: groups of 8
-    v += dpp_f<0x140>(v);                              // row_mirror: rows of 16
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));   // lane ^ 16
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
-           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-}
-
-// one dword of 4 int8 weights -> the 16-bit pairs (elements 0, 1) and (2, 3), exactly
-__device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, f16) {
-    const uint32_t a = d ^ 0x80808080u;
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    p0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) - bias);
-    p1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) - bias);
-}
-__device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, bf16) {
-    const float f0 = (float)(int8_t)(d & 0xff), f1 = (float)(int8_t)((d >> 8) & 0xff);
-    const float f2 = (float)(int8_t)((d >> 16) & 0xff), f3 = (float)(int8_t)(d >> 24);
-    p0 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-    p1 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
-}
-__device__ __forceinline__ float dot2(uint32_t w2, uint32_t x2, float acc, f16) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w2), __builtin_bit_cast(h2, x2), acc, false);
-}
-__device__ __forceinline__ float dot2(uint32_t w2, uint32_t x2, float acc, bf16) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bh2, w2), __builtin_bit_cast(bh2, x2), acc, false);
-}
-
-template <typename T, int M, int CH, bool GATHER>
-__global__ void __launch_bounds__(256) w8a16_dot_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
-                                                        const float* __restrict__ s, const uint16_t* __restrict__ bias,
-                                                        uint16_t* __restrict__ out, int N, int K, int w_rows,
-                                                        const int* __restrict__ rows) {
-    const int lane = threadIdx.x & 63;
-    const int nw = gridDim.x * (blockDim.x >> 6);
-    const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int K16 = K >> 4;
-    const v4i z = {0, 0, 0, 0};
-    v4i xv[M][CH][2];                                    // 16 activations (32 bytes) per chunk and row
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int c = lane + 64 * j;
-            const v4i* src = reinterpret_cast<const v4i*>(x + (long)m * K + c * 16);
-            xv[m][j][0] = c < K16 ? src[0] : z;
-            xv[m][j][1] = c < K16 ? src[1] : z;
-        }
-    auto src_row = [&](int n) { return GATHER ? min(max(rows[n], 0), w_rows - 1) : n; };
-    v4i wb[2][CH];
-    auto load = [&](int buf, int n) {
-        const int8_t* row = w + (long)src_row(n) * K;
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int c = lane + 64 * j;
-            wb[buf][j] = c < K16 ? wload<true>(row + c * 16) : z;
-        }
-    };
-    auto finish = [&](int buf, int n) {
-        float acc[M];
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CH; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {              // weight dword e: elements 4 e .. 4 e + 3 of the chunk
-                uint32_t p0, p1;
-                widen4((uint32_t)wb[buf][j][e], p0, p1, T{});
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    acc[m] = dot2(p0, (uint32_t)xv[m][j][e >> 1][2 * (e & 1)], acc[m], T{});
-                    acc[m] = dot2(p1, (uint32_t)xv[m][j][e >> 1][2 * (e & 1) + 1], acc[m], T{});
-                }
-            }
-        const int sr = src_row(n);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float t = wave_sum_f(acc[m]);
-            if (lane == m) {
-                const float b = bias ? to_float(T{bias[sr]}) : 0.0f;
-                out[(long)m * N + n] = from_float<T>(__builtin_fmaf(t, s[sr], b));
-            }
-        }
-    };
-    int n0 = wid;
-    if (n0 >= N) return;
-    load(0, n0);
-    while (true) {
-        if (n0 + nw < N) load(1, n0 + nw);
-        finish(0, n0);
-        n0 += nw;
-        if (n0 >= N) break;
-        if (n0 + nw < N) load(0, n0 + nw);
-        finish(1, n0);
-        n0 += nw;
-        if (n0 >= N) break;
-    }
-}
-
 // M = 1 up to K = 8192 and M = 2 up to K = 5120 (the activations' registers) take the VALU kernel.
 constexpr int W8A16_DOT_MAX_CH_M1 = 8, W8A16_DOT_MAX_CH_M2 = 5;
 
