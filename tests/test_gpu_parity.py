@@ -430,7 +430,8 @@ def test_i32_stream_kernel(L, M, N, K):
 
 DOT4_SHAPES = [(1, 17408, 5120), (2, 17408, 5120), (1, 1000, 5136), (2, 300, 16), (1, 64, 8192), (2, 33, 48),
                (1, 7, 1040), (1, 5120, 17408), (1, 300, 17408), (1, 129, 9232), (1, 64, 12304), (2, 100, 8192),
-               (3, 17408, 5120), (3, 129, 8192), (3, 5, 48)]
+               (3, 17408, 5120), (3, 129, 8192), (3, 5, 48), (4, 17408, 5120), (5, 300, 5120), (4, 7, 16),
+               (5, 1000, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", DOT4_SHAPES)

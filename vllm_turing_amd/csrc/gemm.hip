@@ -7,9 +7,10 @@
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
 // Four kernels:
-//  * gemv_dot4_kernel, M = 1 and K <= 17408, or M = 2, 3 and K <= 8192 (decode): weight-streaming through the VALU: each
-//    wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against activations held in
-//    registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain (csrc/w8a8_gemv.cu:91).
+//  * gemv_dot4_kernel, M = 1 and K <= 17408, M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120 (decode): weight-streaming
+//    through the VALU: each wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against
+//    activations held in registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain
+//    (csrc/w8a8_gemv.cu:91).
 //  * stream_lds_kernel, the rest of M <= 32 (decode, speculative verify): weight-streaming and HBM-bound.  A workgroup
 //    owns 16 weight rows; its 4 wavefronts take interleaved 128-byte K steps, each through a private LDS ring filled
 //    by direct-to-LDS loads of 1 KB (8 rows x 128 contiguous bytes each), and feed v_mfma_i32_16x16x64_i8 with the
@@ -898,12 +899,13 @@ struct Args {
     hipStream_t st;
 };
 
-// One to three activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
+// One to five activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
 // vs 18.1 us at K = 5120, N = 17408), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two or three rows
-// up to K = 8192 (past that the LDS-ring kernel won, 19.6 vs 22.0 us at K = 17408, M = 2).  Three rows: 17.4 vs
-// 18.4 us at K = 5120, N = 17408; four rows lose (20.2 vs 18.6: the activations' registers halve the occupancy).  Chunk counts are rounded up to the
+// up to K = 8192 (past that the LDS-ring kernel won, 19.6 vs 22.0 us at K = 17408, M = 2), at four or five rows up
+// to K = 5120.  At K = 5120, N = 17408: M=3 16.2 vs 18.4 us, M=4 17.0 vs 18.4, M=5 17.7 vs 18.6; six rows tie and
+// seven or eight lose (19.2 / 21.2 / 21.6 vs 19.0 / 19.1 / 19.5 us: the activations' registers cut occupancy).  Chunk counts are rounded up to the
 // next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
-constexpr int DOT4_MAX_M = 3, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8;
+constexpr int DOT4_MAX_M = 5, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8, DOT4_MAX_CH_M4 = 5;
 
 static int dot4_chunks(int K) {
     const int c = (K / 16 + 63) / 64;
@@ -918,7 +920,7 @@ constexpr int DOT4_BLOCKS_PER_CU = 4;
 
 template <typename T, int M, int CH, int EPI>
 static void launch_dot4_ch(const Args& p) {
-    if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2)) {
+    if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2) && (M < 4 || CH <= DOT4_MAX_CH_M4)) {
         const void* kern = reinterpret_cast<const void*>(&gemv_dot4_kernel<T, M, CH, 1, EPI>);
         static const int occ = [kern] {
             int nb = 0;
@@ -943,7 +945,8 @@ static void launch_dot4_m(const Args& p) {
     }
 }
 static bool dot4_ok(const Args& p) {
-    return p.M <= DOT4_MAX_M && dot4_chunks(p.K) <= (p.M < 2 ? DOT4_MAX_CH : DOT4_MAX_CH_M2);
+    return p.M <= DOT4_MAX_M &&
+           dot4_chunks(p.K) <= (p.M < 2 ? DOT4_MAX_CH : p.M < 4 ? DOT4_MAX_CH_M2 : DOT4_MAX_CH_M4);
 }
 
 template <typename T, int EPI>
@@ -952,6 +955,8 @@ static void launch_dot4(const Args& p) {
         case 1: launch_dot4_m<T, 1, EPI>(p); break;
         case 2: launch_dot4_m<T, 2, EPI>(p); break;
         case 3: launch_dot4_m<T, 3, EPI>(p); break;
+        case 4: launch_dot4_m<T, 4, EPI>(p); break;
+        case 5: launch_dot4_m<T, 5, EPI>(p); break;
     }
 }
 
