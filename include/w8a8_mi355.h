@@ -93,10 +93,17 @@ int w8a16_gemv_rows(const void* x, const void* w, const void* s, const void* bia
 
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
  * checks: kernel 0 the small-M MFMA streaming kernel (M <= 32), 1 the prefill kernel as dispatched, 2 the v_dot4
- * streaming kernel (M = 1 and K <= 17408, or M = 2 and K <= 8192), 3 and 4 the prefill kernel's quarter-tile and
- * full-tile configurations alone.  No counterpart in the reference.  Returns -1 on bad arguments, else the HIP launch
- * error. */
+ * streaming kernel (M = 1 and K <= 17408, M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120), 3 and 4 the prefill
+ * kernel's quarter-tile and full-tile configurations alone.  No counterpart in the reference.  Returns -1 on bad
+ * arguments, else the HIP launch error. */
 int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream);
+
+/* Test export: silu_mul_quant (dtype 0) / silu_mul_quant_bf16 (dtype 1) through one of its two kernels, path 1 the
+ * direct kernel (float32 exp and division per element), path 2 the table kernel (the device's 16-bit silu of every
+ * gate pattern, built once per device, looked up in LDS), so that tests can compare them.  No counterpart in the
+ * reference.  Returns silu_mul_quant's codes, and 1 where the table kernel does not apply (I > 40960, or its table
+ * not yet built while the stream is being captured). */
+int silu_mul_quant_path(const void* gu, void* q, void* scales, int M, int I, int dtype, int path, void* stream);
 
 /* Test export: the device silu of all 65,536 input patterns of dtype, out[65536] uint16 bit patterns.  No
  * counterpart in the reference.  Returns -1 on bad arguments, else the HIP launch error. */

@@ -58,9 +58,10 @@ def test_argument_validation_codes(L):
     assert L.w8a8_big(16, 16, 0, 0, 0, 64, 64, 72, 0, None) == 1                  # K % 16
     assert L.w8a8_scaled_mm(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
     assert L.w8a8_i32(16, 16, 0, 33, 64, 64, 0, None) == -1                       # streaming kernel: M <= 32
-    assert L.w8a8_i32(16, 16, 0, 3, 64, 64, 2, None) == -1                       # VALU kernel: M <= 2
+    assert L.w8a8_i32(16, 16, 0, 6, 64, 64, 2, None) == -1                       # VALU kernel: M <= 5
     assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # K <= 17408 at one row
     assert L.w8a8_i32(16, 16, 0, 2, 64, 8208, 2, None) == -1                     # K <= 8192 at two rows
+    assert L.w8a8_i32(16, 16, 0, 4, 64, 5136, 2, None) == -1                     # K <= 5120 at four rows
     assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 5, None) == -1
     # silu_mul_quant: 1 = bad I, 0 for M == 0 (csrc/silu_quant.cu:72-73)
     assert L.silu_mul_quant(None, None, None, 4, 12, None) == 1
@@ -69,6 +70,9 @@ def test_argument_validation_codes(L):
     assert L.per_token_quant(None, None, None, 4, 16, 16, 0, None) == -1
     assert L.per_token_quant(16, 16, 16, 0, 16, 16, 0, None) == 0
     assert L.silu_table(None, 0, None) == -1
+    assert L.silu_mul_quant_path(16, 16, 16, 4, 16, 2, 1, None) == 1            # dtype
+    assert L.silu_mul_quant_path(16, 16, 16, 4, 16, 0, 0, None) == 1            # path 1 or 2
+    assert L.silu_mul_quant_path(16, 16, 16, 4, 12, 0, 1, None) == 1            # I % 8
     assert L.w8a16_gemv(16, 16, 16, None, 16, 33, 64, 64, 0, None) == -1        # M <= 32
     assert L.w8a16_gemv(16, 16, 16, None, 16, 4, 64, 72, 0, None) == -1         # K % 16
     assert L.w8a16_gemv(16, 16, 16, None, 16, 4, 64, 64, 2, None) == -1         # dtype

@@ -351,8 +351,8 @@ def test_per_token_quant_abi_errors(L):
 # SiLU * up + quant
 # ---------------------------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-# M >= 512 and I <= 40960 take the table kernel (one persistent block per CU): (1680, 8704), (4096, 17408),
-# (600, 136), (513, 8), (520, 40960); (520, 65536) the direct kernel
+# I <= 40960 takes the table kernel (one persistent block per CU, once the table is built), (520, 65536) and (2, 65536)
+# the direct kernel
 @pytest.mark.parametrize("M,I", [(1, 8704), (7, 8704), (1680, 8704), (300, 4096), (5, 136), (4, 17408), (2, 65536),
                                  (4096, 17408), (520, 65536), (600, 136), (513, 8),
                                  (520, 40960)])
@@ -371,25 +371,36 @@ def test_silu_mul_quant(L, dt, M, I):
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 def test_silu_mul_quant_table_exhaustive(L, dt):
-    """Every 16-bit gate pattern (NaN and infinity included) through the table kernel (512 rows of 128) against the
-    direct kernel (the same rows in launches of 64): bit-identical q and scales."""
+    """Every 16-bit gate pattern (NaN and infinity included) through the table kernel against the direct kernel, at
+    512 rows of 128 and at one row of 40960 (the table kernel's longest): bit-identical q and scales; the dispatched
+    entry point equals them; rows longer than 40960 are refused by the table path."""
     say(f"silu table kernel exhaustive {dt}")
     g = torch.Generator().manual_seed(5)
     pat = torch.arange(65536, dtype=torch.int32)
-    gate = torch.where(pat >= 32768, pat - 65536, pat).to(torch.int16).view(dt).view(512, 128)
-    up = (torch.randn(512, 128, generator=g) * 2).to(dt)
-    gu = torch.cat([gate, up], dim=1).contiguous().to(DEV)
-    fn = L.silu_mul_quant if dt == torch.float16 else L.silu_mul_quant_bf16
-    q_t = torch.empty(512, 128, dtype=torch.int8, device=DEV)
-    s_t = torch.empty(512, dtype=torch.float32, device=DEV)
-    assert fn(gu.data_ptr(), q_t.data_ptr(), s_t.data_ptr(), 512, 128, stream()) == 0
-    q_d = torch.empty_like(q_t)
-    s_d = torch.empty_like(s_t)
-    for r0 in range(0, 512, 64):
-        assert fn(gu[r0:].data_ptr(), q_d[r0:].data_ptr(), s_d[r0:].data_ptr(), 64, 128, stream()) == 0
-    torch.cuda.synchronize()
-    assert torch.equal(q_t, q_d), int((q_t != q_d).sum())
-    assert torch.equal(s_t.view(torch.int32), s_d.view(torch.int32))
+    gate = torch.where(pat >= 32768, pat - 65536, pat).to(torch.int16).view(dt)
+    for M, I in ((512, 128), (1, 40960)):
+        gt = gate[: M * I].view(M, I) if M * I <= 65536 else gate[:I].view(1, I)
+        up = (torch.randn(M, I, generator=g) * 2).to(dt)
+        gu = torch.cat([gt, up], dim=1).contiguous().to(DEV)
+        outs = []
+        for path in (1, 2):
+            q = torch.empty(M, I, dtype=torch.int8, device=DEV)
+            s = torch.empty(M, dtype=torch.float32, device=DEV)
+            assert L.silu_mul_quant_path(gu.data_ptr(), q.data_ptr(), s.data_ptr(), M, I, code(dt), path, stream()) == 0
+            outs.append((q, s))
+        fn = L.silu_mul_quant if dt == torch.float16 else L.silu_mul_quant_bf16
+        q0 = torch.empty(M, I, dtype=torch.int8, device=DEV)
+        s0 = torch.empty(M, dtype=torch.float32, device=DEV)
+        assert fn(gu.data_ptr(), q0.data_ptr(), s0.data_ptr(), M, I, stream()) == 0
+        torch.cuda.synchronize()
+        (q_d, s_d), (q_t, s_t) = outs
+        assert torch.equal(q_t, q_d), int((q_t != q_d).sum())
+        assert torch.equal(s_t.view(torch.int32), s_d.view(torch.int32))
+        assert torch.equal(q0, q_t) and torch.equal(s0.view(torch.int32), s_t.view(torch.int32))
+    g2 = torch.zeros(2, 2 * 65536, dtype=dt, device=DEV)
+    qq = torch.empty(2, 65536, dtype=torch.int8, device=DEV)
+    ss = torch.empty(2, dtype=torch.float32, device=DEV)
+    assert L.silu_mul_quant_path(g2.data_ptr(), qq.data_ptr(), ss.data_ptr(), 2, 65536, code(dt), 2, stream()) == 1
 
 
 def test_silu_mul_quant_codes(L):

@@ -25,6 +25,7 @@ SIGNATURES = {
     "rms_norm_quant": [_vp] * 4 + [ctypes.c_float] + [_vp] * 2 + [_i] * 3 + [_vp],
     "w8a8_i32": [_vp] * 3 + [_i] * 4 + [_vp],
     "silu_table": [_vp, _i, _vp],
+    "silu_mul_quant_path": [_vp] * 3 + [_i] * 4 + [_vp],
     "f32_to_16": [_vp, _vp, _l, _i, _vp],
 }
 

@@ -77,6 +77,17 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)d << 24);
 }
 
+// ---- buffer loads straight into LDS ----------------------------------------------------------------------------------
+// s_waitcnt immediate for vmcnt(n) alone (expcnt and lgkmcnt left at their maxima; gfx9 encoding).
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70 | 0xf00; }
+
+// Raw buffer descriptor over `bytes` bytes (callers keep every offset within 31 bits).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
 // ---- wavefront (64-lane) reductions ----------------------------------------------------------------------------------
 // DPP row operations combine lanes inside each 16-lane row, ds_swizzle combines the two rows of each 32-lane half,
 // and the two halves meet through readlane.  max and integer add are exact, so the order is free.

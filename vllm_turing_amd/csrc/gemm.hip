@@ -226,13 +226,6 @@ __device__ __forceinline__ int swz(int row) {
     else return (row ^ ((row >> 3) & 1)) & 7;
 }
 
-// s_waitcnt immediate for vmcnt(n) alone (expcnt and lgkmcnt left at their maxima; gfx9 encoding).
-constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70 | 0xf00; }
-
-// Raw buffer descriptor over `bytes` bytes (the host checks that M * K and N * K fit 31-bit offsets).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 // Raw int32 store of one wavefront's (32 FM) x (32 FN) block (test export only): straight from the fragment layout.
 template <int FM, int FN>
@@ -346,7 +339,6 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
     }
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
 constexpr int CPOL_NT = 2;                                // cache-policy operand of a buffer load: non-temporal
 
 // One K stage of a wavefront's share of A and W (bpw 1 KB blocks of each), straight into LDS.  Block j's lane reads
