@@ -102,10 +102,10 @@ def _ulp16_t(v, dt):
     return 2.0 ** (e - mant)
 
 
-# M = 1 (K <= 8192) and M = 2 (K <= 5120) take the VALU kernel, the rest the MFMA kernel
+# M = 1 (K <= 8192) and M = 2, 3 (K <= 5120) take the VALU kernel, the rest the MFMA kernel
 W8A16_CASES = [(1, 17408, 5120), (4, 4096, 5120), (16, 1000, 2048), (5, 333, 4112), (32, 2048, 1024), (17, 64, 16),
                (3, 248320 // 8, 5120), (2, 1000, 2048), (1, 7, 16), (1, 333, 8192), (2, 129, 5120), (1, 100, 8208),
-               (2, 31, 5136)]
+               (2, 31, 5136), (3, 777, 5120), (3, 64, 1024)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
@@ -139,7 +139,7 @@ def test_w8a16(L, dt, M, N, K):
         else ((got - exact).abs() / (exact.abs() + 1e-3 * exact.abs().max())).max() < 2e-3
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3])
 def test_w8a16_rows_small_m(L, M):
     """Gathered rows (repeats, the first and last row) on the VALU kernel equal the dense logits' columns."""
     say(f"w8a16 rows M={M}")
