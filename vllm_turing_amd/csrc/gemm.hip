@@ -1146,7 +1146,7 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
 // W8A16 (int8 LM head)
 // ---------------------------------------------------------------------------------------------------------------------
 // M = 1 up to K = 8192 and M = 2, 3 up to K = 5120 (the activations' registers) take the VALU kernel (M = 3 at
-// N = 248320: 289 -> 229 us; four rows need every register of the SIMD and lose, 298 -> 387 us).
+// N = 248320: 289 -> 229 us; four rows take 256 registers, one wavefront per SIMD, and lose: 298 -> 387 us).
 constexpr int W8A16_DOT_MAX_CH_M1 = 8, W8A16_DOT_MAX_CH_M2 = 5;
 
 template <typename T, int M, int CH, bool GATHER>
