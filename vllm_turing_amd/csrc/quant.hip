@@ -470,6 +470,17 @@ static int pick_threads(int nvec, int max_vpt, int* vpt) {
     return t;
 }
 
+
+// Fewer rows than CUs: as many threads per row as it has vectors (up to 1024), so that each thread's serial share
+// of the row is small (M = 1, K = 5120: per-token quant 2.9 -> 2.2 us, RMSNorm + quant 4.5 -> 3.8 us).
+static int pick_threads_m(int nvec, int max_vpt, int* vpt, int M) {
+    if (M >= 256) return pick_threads(nvec, max_vpt, vpt);
+    int t = (nvec + 63) / 64 * 64;
+    if (t < 64) t = 64;                                   // nvec = 0 (K < 8): the any-K kernel takes the row
+    if (t > 1024) t = 1024;
+    *vpt = (nvec + t - 1) / t;
+    return t;
+}
 template <typename T, int VPT>
 static void launch_ptq(const uint16_t* x, int8_t* q, float* s, int M, int K, long ldx, int threads, hipStream_t st) {
     per_token_quant_kernel<T, VPT><<<M, threads, 0, st>>>(x, q, s, K, ldx);
@@ -482,7 +493,7 @@ static int run_ptq(const void* x, void* q, void* s, int M, int K, long ldx, hipS
     float* sp = static_cast<float*>(s);
     const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
     int vpt = 0;
-    const int threads = pick_threads(K / 8, MAX_VPT_QUANT, &vpt);
+    const int threads = pick_threads_m(K / 8, MAX_VPT_QUANT, &vpt, M);
     if (!vec_ok || vpt > MAX_VPT_QUANT) {
         per_token_quant_any_kernel<T><<<M, 256, 0, st>>>(xp, qp, sp, K, ldx);
         return 0;
@@ -591,7 +602,7 @@ static int run_rnq_res(const void* x, void* res, const void* w, const float* ub,
     int8_t* qp = static_cast<int8_t*>(q);
     float* sp = static_cast<float*>(s);
     int vpt = 0;
-    const int threads = pick_threads(K / 8, MAX_VPT_NORM, &vpt);
+    const int threads = pick_threads_m(K / 8, MAX_VPT_NORM, &vpt, M);
     switch (vpt) {
 #define W8_CASE(V) case V: rms_norm_quant_kernel<T, V, RES><<<M, threads, 0, st>>>(xp, rp, wp, ub, eps, qp, sp, K); break;
         W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6)
