@@ -672,13 +672,25 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
     }
     const int nsteps = (K + 127) >> 7;
     const int mine = ks < nsteps ? (nsteps - 1 - ks) / KS + 1 : 0;
-    auto issue = [&](int i) {
-        dma_step(rsw, rsw, ring + (i % NS) * STEP_BYTES, off, chk, LPS, (ks + i * KS) * 128, K);
+    const int r = lane & 15, g = lane >> 4;
+    // The step's activation fragments are loaded with its weights, into a register ring beside the LDS ring, from
+    // clamped (in-bounds) addresses and masked where used: loaded where used, under the m < M && k < K condition, each
+    // was waited for before its MFMA.
+    uint4 xr[NS][4][MT];
+    auto issue = [&](int i, int slot) {
+        const int k0 = (ks + i * KS) * 128;
+        dma_step(rsw, rsw, ring + slot * STEP_BYTES, off, chk, LPS, k0, K);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = min(mt * 16 + r, M - 1), k = min(k0 + 32 * j + 8 * g, K - 8);
+                xr[slot][j][mt] = *reinterpret_cast<const uint4*>(x + (long)m * K + k);
+            }
     };
     f4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int r = lane & 15, g = lane >> 4;
     auto compute = [&](int slot, int k0) {
         const uint8_t* st = ring + slot * STEP_BYTES;
 #pragma unroll
@@ -689,8 +701,7 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int m = mt * 16 + r;
-                const uint4 xv = m < M && k < K ? *reinterpret_cast<const uint4*>(x + (long)m * K + k)
-                                                : make_uint4(0, 0, 0, 0);
+                const uint4 xv = m < M && k < K ? xr[slot][j][mt] : make_uint4(0, 0, 0, 0);
                 if constexpr (__is_same(T, f16))
                     acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(widen_f16(wv.x, wv.y),
                                                                      __builtin_bit_cast(h8, xv), acc[mt], 0, 0, 0);
@@ -700,17 +711,24 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
             }
         }
     };
-    constexpr int WAIT2 = waitcnt_vm(2 * LPS), WAIT1 = waitcnt_vm(LPS), WAIT0 = waitcnt_vm(0);
+    constexpr int VPS = LPS + 4 * MT;                    // vector memory instructions per step
+    constexpr int WAIT2 = waitcnt_vm(2 * VPS), WAIT1 = waitcnt_vm(VPS), WAIT0 = waitcnt_vm(0);
+    static_assert(NS == 3, "the register ring is unrolled for three steps");
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
-        if (i < mine) issue(i);
-    for (int i = 0; i < mine; ++i) {
-        const int ahead = min(mine - 1 - i, NS - 2);
-        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
-        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAIT1);
-        else __builtin_amdgcn_s_waitcnt(WAIT0);
-        if (i + NS - 1 < mine) issue(i + NS - 1);
-        compute(i % NS, (ks + i * KS) * 128);
+        if (i < mine) issue(i, i);
+    for (int i0 = 0; i0 < mine; i0 += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {                   // step i in slot u (i0 is a multiple of NS)
+            const int i = i0 + u;
+            if (i >= mine) break;
+            const int ahead = min(mine - 1 - i, NS - 2);
+            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
+            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAIT1);
+            else __builtin_amdgcn_s_waitcnt(WAIT0);
+            if (i + NS - 1 < mine) issue(i + NS - 1, (u + NS - 1) % NS);
+            compute(u, (ks + i * KS) * 128);
+        }
     }
     // K slices meet in LDS, in slice order
     __syncthreads();
