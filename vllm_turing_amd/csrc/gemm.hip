@@ -66,18 +66,12 @@ __device__ __forceinline__ v4i wload(const int8_t* p) {
     else return *reinterpret_cast<const v4i*>(p);
 }
 
-// ---------------------------------------------------------------------------------------------------------------------
-// gemv_dot4_kernel: M <= 4 activation rows, weights streamed once through the VALU
-// ---------------------------------------------------------------------------------------------------------------------
-// Every wavefront instruction reads 1 KB of one weight row (64 lanes x 16 contiguous bytes); lane l owns the 16-byte
-// chunks l, l + 64, ... of every row (CH of them), and keeps the matching activation chunks of all M rows in
-// registers for the whole kernel.  Rows are grid-strided over the wavefronts, R rows per iteration with the next
-// iteration's loads issued before this one's v_dot4 math (double buffering).  Each row's per-lane partial sums are
-// reduced across the wavefront with DPP row operations, ds_swizzle and readlane.
+// Four 16-bit zeros: the bias operand of a 4-column group without bias.
+__device__ __align__(16) const uint16_t g_zero4[4] = {0, 0, 0, 0};
 // A 16-bit zero in device memory: the bias operand of a row without bias, so that the bias load is unconditional.
 __device__ const uint16_t g_zero16 = 0;
 
-// The same with the scales and bias already in registers.
+// Output write of one element as store_out, with the scales and bias already in registers.
 template <typename T, int EPI>
 __device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sam, float swn, float bn) {
     if constexpr (EPI == EPI_I32) {
@@ -91,6 +85,14 @@ __device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sa
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------------
+// gemv_dot4_kernel: M <= 5 activation rows, weights streamed once through the VALU
+// ---------------------------------------------------------------------------------------------------------------------
+// Every wavefront instruction reads 1 KB of one weight row (64 lanes x 16 contiguous bytes); lane l owns the 16-byte
+// chunks l, l + 64, ... of every row (CH of them), and keeps the matching activation chunks of all M rows in
+// registers for the whole kernel.  Rows are grid-strided over the wavefronts, R rows per iteration with the next
+// iteration's loads issued before this one's v_dot4 math (double buffering).  Each row's per-lane partial sums are
+// reduced across the wavefront with DPP row operations, ds_swizzle and readlane.
 template <typename T, int M, int CH, int R, int EPI, bool NT = true>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
@@ -266,6 +268,22 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
     float sam[FM];
 #pragma unroll
     for (int i = 0; i < FM; ++i) sam[i] = sa[sa_rows ? min(mb + i * 32 + (lane & 31), M - 1) : 0];
+    // per-column scales and bias: with N % 4 == 0, every 4-column group of this wavefront at once, unconditionally
+    // (the last group clamped in bounds; its columns past N are never stored), before any is used (~1%)
+    const bool has_bias = (EPI == EPI_LARGE_BIAS || EPI == EPI_SMALL) && bias != nullptr;
+    const bool vec_cols = (N & 3) == 0 && sw_rows;
+    float4 sw4[FN][4];
+    uint2 b2[FN][4];
+    if (vec_cols) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = min(nb + j * 32 + 8 * q + 4 * (lane >> 5), N - 4);
+                sw4[j][q] = *reinterpret_cast<const float4*>(sw + n);
+                b2[j][q] = *reinterpret_cast<const uint2*>(has_bias ? bias + n : g_zero4);
+            }
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -273,18 +291,11 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
             const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
             const int n = nb + nl;
             float swv[4], bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            const bool has_bias = (EPI == EPI_LARGE_BIAS || EPI == EPI_SMALL) && bias != nullptr;
-            if (n + 3 < N && (N & 3) == 0) {                 // four whole columns: vector loads
-                if (sw_rows) {
-                    const float4 t = *reinterpret_cast<const float4*>(sw + n);
-                    swv[0] = t.x; swv[1] = t.y; swv[2] = t.z; swv[3] = t.w;
-                } else {
-                    swv[0] = swv[1] = swv[2] = swv[3] = sw[0];
-                }
+            if (vec_cols) {
+                swv[0] = sw4[j][q].x; swv[1] = sw4[j][q].y; swv[2] = sw4[j][q].z; swv[3] = sw4[j][q].w;
                 if (has_bias) {
-                    const uint2 t = *reinterpret_cast<const uint2*>(bias + n);
-                    bv[0] = lo_half(t.x, T{}); bv[1] = hi_half(t.x, T{});
-                    bv[2] = lo_half(t.y, T{}); bv[3] = hi_half(t.y, T{});
+                    bv[0] = lo_half(b2[j][q].x, T{}); bv[1] = hi_half(b2[j][q].x, T{});
+                    bv[2] = lo_half(b2[j][q].y, T{}); bv[3] = hi_half(b2[j][q].y, T{});
                 }
             } else {
 #pragma unroll
