@@ -13,7 +13,9 @@
 // r = RN_T(float(silu(g)) * float(u)) with silu(g) = RN_T(f / (1 + expf(-f))) as csrc/silu_quant.cu:11-14,39 does.
 // silu depends only on the 16-bit input, so it is checked exhaustively: on all 65,536 fp16 and all 65,536 bf16 inputs
 // the float32 result of this expression is within 2 float32 ulps of the one built on a correctly rounded exp and
-// rounds to the same 16-bit value (GPU test against the oracle's table).
+// rounds to the same 16-bit value (GPU test against the oracle's table).  For the same reason the SiLU kernel that
+// normally runs looks silu up in a table of the device's own 16-bit results for all 65,536 inputs, built once per
+// device with the expression above and held in LDS: bit-identical to evaluating it, at a third of the VALU work.
 //
 // A third kernel fuses the residual add and the RMSNorm in front of the quantization (vLLM's
 // rms_norm_dynamic_per_token_quant as vllm_turing/tailoverlap.py:145 calls it): s = x + r (float), r <- RN_T(s),
