@@ -899,18 +899,6 @@ __global__ void __launch_bounds__(256) w8a16_dot_kernel(const uint16_t* __restri
 // ---------------------------------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------------------------------
-// Compute units of the current device (cached per device).
-static int cu_count() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cached[dev] = v;
-    }
-    return cached[dev];
-}
 
 struct Args {
     const int8_t* a;

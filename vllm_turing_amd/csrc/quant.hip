@@ -540,24 +540,13 @@ static bool silu_lut_ready(int dt, hipStream_t st) {
     return true;
 }
 
-static int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cached[dev] = v;
-    }
-    return cached[dev];
-}
 
 template <typename T, int VPT>
 static void launch_smq_lut(const uint16_t* gp, int8_t* qp, float* sp, int M, int I, int threads, hipStream_t st) {
     const void* kern = reinterpret_cast<const void*>(&silu_mul_quant_lut_kernel<T, VPT>);
     static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, LUT_LDS_BYTES);
     (void)attr;
-    const int grid = M < device_cus() ? M : device_cus();
+    const int grid = M < cu_count() ? M : cu_count();
     silu_mul_quant_lut_kernel<T, VPT><<<grid, threads, LUT_LDS_BYTES, st>>>(gp, qp, sp, M, I);
 }
 
