@@ -930,18 +930,21 @@ static int dot4_chunks(int K) {
 // ordinary loads (the non-temporal loads alone: 15.1 and 17.6 us).
 constexpr int DOT4_BLOCKS_PER_CU = 4;
 
+// Workgroups per CU of a row-streaming VALU kernel (256 threads, no LDS): DOT4_BLOCKS_PER_CU, or as many as are
+// resident together if fewer (its caller keeps the answer in a static per kernel).
+static int row_stream_per_cu(const void* kern) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
+    return nb < DOT4_BLOCKS_PER_CU ? nb : DOT4_BLOCKS_PER_CU;
+}
+
 template <typename T, int M, int CH, int EPI>
 static void launch_dot4_ch(const Args& p) {
     if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2) && (M < 4 || CH <= DOT4_MAX_CH_M4)) {
-        const void* kern = reinterpret_cast<const void*>(&gemv_dot4_kernel<T, M, CH, 1, EPI>);
-        static const int occ = [kern] {
-            int nb = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
-            return nb;
-        }();
-        const int per_cu = occ < DOT4_BLOCKS_PER_CU ? occ : DOT4_BLOCKS_PER_CU;
-        const int need = (p.N + 3) / 4, full = cu_count() * per_cu;
-        gemv_dot4_kernel<T, M, CH, 1, EPI><<<need < full ? need : full, 256, 0, p.st>>>(
+        static const int per_cu =
+            row_stream_per_cu(reinterpret_cast<const void*>(&gemv_dot4_kernel<T, M, CH, 1, EPI>));
+        const int need = (p.N + 3) / 4, grid = cu_count() * per_cu;
+        gemv_dot4_kernel<T, M, CH, 1, EPI><<<need < grid ? need : grid, 256, 0, p.st>>>(
             p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
     }
 }
@@ -1172,15 +1175,9 @@ constexpr int W8A16_DOT_MAX_CH_M1 = 8, W8A16_DOT_MAX_CH_M2 = 5;
 template <typename T, int M, int CH, bool GATHER>
 static void launch_w8a16_dot_t(const void* x, const void* w, const void* s, const void* bias, void* out, int N, int K,
                                int w_rows, const int* rows, hipStream_t st) {
-    const void* kern = reinterpret_cast<const void*>(&w8a16_dot_kernel<T, M, CH, GATHER>);
-    static const int occ = [kern] {
-        int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
-        return nb;
-    }();
-    const int per_cu = occ < DOT4_BLOCKS_PER_CU ? occ : DOT4_BLOCKS_PER_CU;
-    const int need = (N + 3) / 4, full = cu_count() * per_cu;
-    w8a16_dot_kernel<T, M, CH, GATHER><<<need < full ? need : full, 256, 0, st>>>(
+    static const int per_cu = row_stream_per_cu(reinterpret_cast<const void*>(&w8a16_dot_kernel<T, M, CH, GATHER>));
+    const int need = (N + 3) / 4, grid = cu_count() * per_cu;
+    w8a16_dot_kernel<T, M, CH, GATHER><<<need < grid ? need : grid, 256, 0, st>>>(
         static_cast<const uint16_t*>(x), static_cast<const int8_t*>(w), static_cast<const float*>(s),
         static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), N, K, w_rows, rows);
 }
