@@ -915,8 +915,8 @@ struct Args {
 // vs 18.1 us at K = 5120, N = 17408), at one row up to K = 17408 (17.5 vs 19.4 us at N = 5120), at two or three rows
 // up to K = 8192 (past that the LDS-ring kernel won, 19.6 vs 22.0 us at K = 17408, M = 2), at four or five rows up
 // to K = 5120.  At K = 5120, N = 17408: M=3 16.2 vs 18.4 us, M=4 17.0 vs 18.4, M=5 17.7 vs 18.6; six rows tie and
-// seven or eight lose (19.2 / 21.2 / 21.6 vs 19.0 / 19.1 / 19.5 us: the activations' registers cut occupancy).  Chunk counts are rounded up to the
-// next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
+// seven or eight lose (19.2 / 21.2 / 21.6 vs 19.0 / 19.1 / 19.5 us: the activations' registers cut occupancy).
+// Chunk counts are rounded up to the next of 1..8, 10, 12, 14, 17 (chunks past K are masked).
 constexpr int DOT4_MAX_M = 5, DOT4_MAX_CH = 17, DOT4_MAX_CH_M2 = 8, DOT4_MAX_CH_M4 = 5;
 
 static int dot4_chunks(int K) {
