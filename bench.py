@@ -9,7 +9,9 @@ is GPU work only (HIP events on the launch stream, bracketed by synchronizations
 
 Also reported:
   decode_other_m: the same GEMV at M = 2, 4, 8;
-  gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline);
+  gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline),
+    with the median gfx clock amd-smi reports during a 2 s run of it (sclk_mhz) and the fraction of the peak scaled
+    to that clock (frac_at_sclk; the 5.0 POP/s peak is quoted at 2400 MHz);
   quant: per-token quant at M=4096, K=5120, SiLU*up+quant at M=4096, I=17408, and the AR8 all-reduce operand
     (quantize; dequantised sum of 2 and 8 ranks) at 4096 x 5120, in GB/s (HBM-bound);
   lm_head_w8a16: the int8 LM head (W8A16) over a 248,320 x 5120 vocabulary at M = 1, 4, 16, GB/s (HBM-bound);
@@ -42,6 +44,7 @@ if ROOT not in sys.path:
 METRIC = "W8A8 GEMM TOPS @M=4096 + GEMV HBM GB/s @M=1 (1×MI355X, % roofline)"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+SCLK_MAX_MHZ = 2400.0          # the gfx clock that peak is quoted at
 
 
 def traffic_from_profiles(key):
@@ -86,6 +89,50 @@ def graph_time(torch, launch, n_launch_per_graph, steps, warmup):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
     return ms / (reps * n_launch_per_graph), reps * n_launch_per_graph
+
+
+def sclk_under_load(torch, launch, seconds=2.0):
+    """Median gfx clock in MHz (over the XCDs and the samples) that `amd-smi metric -c` reports while `launch` runs
+    back to back for about `seconds`; None when amd-smi is absent or its output does not parse.  The dense int8
+    MFMA peak (5.0 POP/s) is quoted at the 2400 MHz maximum; under a sustained GEMM the clock sits lower."""
+    import shutil
+    import subprocess
+    import threading
+    exe = shutil.which("amd-smi")
+    if exe is None:
+        return None
+    clocks, stop = [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            try:
+                r = subprocess.run([exe, "metric", "-g", "0", "-c", "--json"], capture_output=True, text=True,
+                                   timeout=20)
+                d = json.loads(r.stdout)
+                d = d["gpu_data"] if isinstance(d, dict) else d
+                for key, c in d[0]["clock"].items():
+                    if key.startswith("gfx_") and isinstance(c.get("clk"), dict):
+                        v = c["clk"].get("value")
+                        if isinstance(v, (int, float)) and v > 0:
+                            clocks.append(float(v))
+            except (OSError, ValueError, KeyError, IndexError, TypeError, subprocess.SubprocessError):
+                return
+
+    th = threading.Thread(target=poll, daemon=True)
+    t_end = time.time() + seconds
+    launch()
+    torch.cuda.synchronize()
+    th.start()
+    while time.time() < t_end:
+        for _ in range(20):
+            launch()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=30)
+    if not clocks:
+        return None
+    clocks.sort()
+    return clocks[len(clocks) // 2]
 
 
 def cpu_time(fn, budget_s):
@@ -357,6 +404,8 @@ def bench_headline(torch, L, st, dev, args):
     gemm_ops = 2.0 * Mg * Ng * Kg
     gemm_tops = gemm_ops / (ms_gemm * 1e-3) / 1e12
     print(f"[bench] GEMM {ms_gemm * 1e3:.1f} us/launch, {gemm_tops:.0f} TOPS", file=sys.stderr, flush=True)
+    sclk = sclk_under_load(torch, lambda: gemm(0))
+    print(f"[bench] gfx clock under GEMM load: {sclk} MHz", file=sys.stderr, flush=True)
 
     # ---- quant kernels ------------------------------------------------------------------------------------------------
     xq_in = torch.randn(Mg, Kg, dtype=torch.bfloat16, device=dev)
@@ -474,6 +523,8 @@ def bench_headline(torch, L, st, dev, args):
                  "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS,
                               "unit": "TOPS", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
                               "traffic": traffic_from_profiles("gemm_m4096")},
+                 "sclk_mhz": sclk,
+                 "frac_at_sclk": (round(gemm_tops / (INT8_PEAK_TOPS * sclk / SCLK_MAX_MHZ), 4) if sclk else None),
                  "cpu_baseline": cpu_gemm},
         "quant": {"per_token_quant_M4096_K5120": {"us": round(ms_q * 1e3, 2),
                                                    "gbs": round(quant_bytes / (ms_q * 1e-3) / 1e9, 1)},
