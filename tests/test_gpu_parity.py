@@ -593,8 +593,9 @@ def test_decode_config_full(L, M):
 
 @pytest.mark.parametrize("M", [512, 4096])
 def test_prefill_config_sampled(L, M):
-    """C3 at full size: every row of the int32 result is checked on a sample of rows (first, last, random) and the
-    whole result through a linearity property: acc(a1 + a2) == acc(a1) + acc(a2) when no int8 overflows."""
+    """The prefill GEMM at K = 5120, N = 12288: every row of the int32 result is checked on a sample of rows (first,
+    last, random) and the whole result through a linearity property: acc(a1 + a2) == acc(a1) + acc(a2) when no int8
+    overflows."""
     say(f"prefill config M={M}")
     from vllm_turing_amd import workloads, per_token_quant, cutlass_scaled_mm
     c = workloads.prefill(M)
