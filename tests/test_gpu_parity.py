@@ -493,6 +493,23 @@ def test_i32_extreme_values(L):
         assert np.array_equal(got, oracle.gemm_i32(aa.numpy(), ww.numpy()))
 
 
+def test_i32_max_k(L):
+    """The largest K the kernels take (131056, K % 16 == 0 and K < 131072): all -128 activations against rows of -128
+    and 127 give sums of 2147221504 and -2130446336, within 0.01% of the int32 range, in every matmul kernel that
+    takes this K (streaming at M = 8 and 32, prefill as dispatched, quarter-tile and full-tile alone)."""
+    say("i32 max K")
+    K = 131056
+    a = torch.full((40, K), -128, dtype=torch.int8)
+    w = torch.full((64, K), -128, dtype=torch.int8)
+    w[1::2] = 127
+    want = np.where(np.arange(64) % 2 == 0, 131056 * 16384, 131056 * -16256).astype(np.int64)
+    assert want.max() < 2 ** 31 and want.min() >= -2 ** 31
+    wd = w.to(DEV)
+    for kernel, m in ((0, 8), (0, 32), (1, 40), (3, 40), (4, 40)):
+        got = i32(L, a[:m].to(DEV), wd, kernel)
+        assert np.array_equal(got, np.broadcast_to(want, (m, 64))), (kernel, m)
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # scaled matmul outputs through the dispatch: bit-exact against the oracle's epilogue for that path
 # ---------------------------------------------------------------------------------------------------------------------
