@@ -928,11 +928,18 @@ static int dot4_chunks(int K) {
     return c <= 8 ? c : c <= 10 ? 10 : c <= 12 ? 12 : c <= 14 ? 14 : c <= 17 ? 17 : 1 << 20;
 }
 
-// Grid: at most DOT4_BLOCKS_PER_CU workgroups per CU that are resident together (fewer when the registers of a long K
-// allow fewer), the same number on every CU, rows grid-strided over their wavefronts.  At K = 5120, N = 17408 with
+// Grid for M >= 3: at most DOT4_BLOCKS_PER_CU workgroups per CU that are resident together (fewer when the registers
+// of a long K allow fewer), the same number on every CU, rows grid-strided over their wavefronts.  At K = 5120, N = 17408 with
 // non-temporal weight loads: M=1 16.9 -> 15.1 us, M=2 19.3 -> 15.8 us against one wavefront per two rows with
 // ordinary loads (the non-temporal loads alone: 15.1 and 17.6 us).
 constexpr int DOT4_BLOCKS_PER_CU = 4;
+// M <= 2 instead: one wavefront per workgroup and ceil(N / DOT4_ROWS_PER_WAVE) of them, so that every wavefront has
+// the same number of rows (four workgroups of four wavefronts per CU leave 4.25 rows per wavefront at N = 17408, a
+// last quarter-round with a quarter of the wavefronts).  Against that grid, two runs at K = 5120: N = 17408 M=1
+// 14.93-14.98 -> 14.73-14.77 us, M=2 15.57 -> 15.40 us; N = 34816 M=1 27.8 -> 27.2 us, M=2 28.4 -> 27.4 us; and
+// N = 5120, K = 17408, M=1 15.7 -> 15.5 us.  Two or four rows per wavefront: as fast at M = 1, K = 5120, up to 6%
+// slower elsewhere; at M = 3 the registers allow fewer wavefronts and this grid is 13% slower.
+constexpr int DOT4_ROWS_PER_WAVE = 3;
 
 // Workgroups per CU of a row-streaming VALU kernel (256 threads, no LDS): DOT4_BLOCKS_PER_CU, or as many as are
 // resident together if fewer (its caller keeps the answer in a static per kernel).
@@ -945,6 +952,12 @@ static int row_stream_per_cu(const void* kern) {
 template <typename T, int M, int CH, int EPI>
 static void launch_dot4_ch(const Args& p) {
     if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2) && (M < 4 || CH <= DOT4_MAX_CH_M4)) {
+        if constexpr (M <= 2) {
+            const int waves = (p.N + DOT4_ROWS_PER_WAVE - 1) / DOT4_ROWS_PER_WAVE;
+            gemv_dot4_kernel<T, M, CH, 1, EPI><<<waves, 64, 0, p.st>>>(
+                p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
+            return;
+        }
         static const int per_cu =
             row_stream_per_cu(reinterpret_cast<const void*>(&gemv_dot4_kernel<T, M, CH, 1, EPI>));
         const int need = (p.N + 3) / 4, grid = cu_count() * per_cu;
