@@ -425,7 +425,10 @@ def i32(L, a, w, kernel):
 STREAM_SHAPES = [(1, 64, 128), (1, 17408, 5120), (2, 1000, 5136), (3, 300, 5168), (4, 256, 16), (8, 17408, 5120),
                  (2, 5120, 17408), (3, 17408, 5120), (16, 17408, 5120), (32, 17408, 5120), (20, 5120, 17408),
                  (13, 7168, 5120), (16, 5120, 8704), (17, 40, 4112), (25, 5120, 3072), (32, 300, 5168),
-                 (31, 8, 48), (1, 5120, 17408), (4, 5120, 6144), (4, 16384, 5120)]
+                 (31, 8, 48), (1, 5120, 17408), (4, 5120, 6144), (4, 16384, 5120),
+                 # tile counts whose last round of four-wavefront workgroups would be under half full: two-wavefront
+                 # workgroups with 3- or 2-step rings, short and ragged K (one wavefront with no K step at K = 16)
+                 (12, 13312, 272), (24, 17408, 1040), (9, 13328, 16), (17, 13312, 5136)]
 
 
 @pytest.mark.parametrize("M,N,K", STREAM_SHAPES)

@@ -542,12 +542,11 @@ __device__ __forceinline__ void dma_step(__amdgpu_buffer_rsrc_t rsw, __amdgpu_bu
     }
 }
 
-template <typename T, int MT, int NS, int EPI>
+template <typename T, int MT, int NS, int EPI, int KS = 4>
 __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                          const float* __restrict__ sa, const float* __restrict__ sw,
                                                          const uint16_t* __restrict__ bias, void* __restrict__ out,
                                                          int M, int N, int K, int sa_rows, int sw_rows) {
-    constexpr int KS = 4;                                // wavefronts per tile
     constexpr int ROWS = 16 + 16 * MT;                   // staged rows per step
     constexpr int STEP_BYTES = ROWS * 128;
     constexpr int LPS = ROWS / 8;                        // 1 KB loads per step
@@ -995,16 +994,44 @@ static void launch_dot4(const Args& p) {
 // M <= 32 past the VALU kernel: the MFMA kernel through per-wavefront LDS rings of 3 steps (48 or 72 KB per
 // workgroup: three or two workgroups per CU); measured against 2 and 4 steps, and against loads straight into
 // registers (the LDS rings take M = 8, K = 5120, N = 17408 from 23.6 to 18.9 us and M = 32 from 45.6 to 28.1 us).
-constexpr int SLDS_NS = 3;
+// One workgroup per 16-row tile: where the tiles need more than one round of the resident workgroups and the last
+// round would be less than half full (a quarter-full last round ran at ~40% of the bandwidth: at M = 8, N = 13312
+// took 16.9 us against 12.6 us at N = 12288), a workgroup of two wavefronts (K in two slices) with a 3-step ring, or
+// else a 2-step ring, is used if that fits every tile in one round: K = 5120, N = 17408, M = 8 19.6 -> 18.4 us,
+// M = 16 21.9 -> 20.9 us, M = 32 30.9 -> 27.4 us.  Where four wavefronts already fill their rounds the narrower
+// workgroups are slower (N = 5120, K = 17408, M = 8: 20.4 -> 29.1 us).
+template <typename T, int MT, int NS, int KS, int EPI>
+struct SldsCfg {
+    static constexpr int LDS = KS * NS * (16 + 16 * MT) * 128;
+    static_assert(LDS <= 160 * 1024, "LDS ring size");
+    static const void* kern() { return reinterpret_cast<const void*>(&stream_lds_kernel<T, MT, NS, EPI, KS>); }
+    static int slots() {                                 // resident workgroups on the whole GPU
+        static const int n = [] {
+            (void)hipFuncSetAttribute(kern(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+            int nb = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern(), 64 * KS, LDS) != hipSuccess || nb < 1) nb = 1;
+            return nb * cu_count();
+        }();
+        return n;
+    }
+    static void launch(const Args& p) {
+        static const hipError_t attr = hipFuncSetAttribute(kern(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        (void)attr;
+        stream_lds_kernel<T, MT, NS, EPI, KS><<<(p.N + 15) / 16, 64 * KS, LDS, p.st>>>(
+            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows);
+    }
+};
 template <typename T, int MT, int EPI>
 static void launch_stream_lds(const Args& p) {
-    constexpr int LDS = 4 * SLDS_NS * (16 + 16 * MT) * 128;
-    static_assert(LDS <= 160 * 1024, "LDS ring size");
-    const void* kern = reinterpret_cast<const void*>(&stream_lds_kernel<T, MT, SLDS_NS, EPI>);
-    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
-    (void)attr;
-    stream_lds_kernel<T, MT, SLDS_NS, EPI><<<(p.N + 15) / 16, 256, LDS, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out,
-                                                                               p.M, p.N, p.K, p.sa_rows, p.sw_rows);
+    using Wide = SldsCfg<T, MT, 3, 4, EPI>;
+    using Two = SldsCfg<T, MT, 3, 2, EPI>;
+    using TwoShort = SldsCfg<T, MT, 2, 2, EPI>;
+    const int tiles = (p.N + 15) / 16, s0 = Wide::slots(), last = tiles % s0;
+    if (tiles > s0 && last > 0 && 2 * last < s0) {
+        if (tiles <= Two::slots()) return Two::launch(p);
+        if (tiles <= TwoShort::slots()) return TwoShort::launch(p);
+    }
+    Wide::launch(p);
 }
 
 // M <= 32: the VALU kernel where it applies, else the LDS-ring MFMA streaming kernel.
