@@ -105,7 +105,9 @@ def _ulp16_t(v, dt):
 # M = 1 (K <= 8192) and M = 2, 3 (K <= 5120) take the VALU kernel, the rest the MFMA kernel
 W8A16_CASES = [(1, 17408, 5120), (4, 4096, 5120), (16, 1000, 2048), (5, 333, 4112), (32, 2048, 1024), (17, 64, 16),
                (3, 248320 // 8, 5120), (2, 1000, 2048), (1, 7, 16), (1, 333, 8192), (2, 129, 5120), (1, 100, 8208),
-               (2, 31, 5136), (3, 777, 5120), (3, 64, 1024)]
+               (2, 31, 5136), (3, 777, 5120), (3, 64, 1024),
+               # two (M <= 16) or three (M > 16) 16-row tiles per workgroup, N not a multiple of either
+               (8, 31, 5136), (24, 4099, 1040), (12, 48 * 7 + 17, 272)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])

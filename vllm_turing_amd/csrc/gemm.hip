@@ -529,11 +529,11 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 // rows, each 128 bytes with the 8-chunk swizzle), so a wavefront only waits for its own loads and no barrier runs in
 // the main loop.  Activation rows past M and K chunks past K are loaded from outside the buffer, which writes zeros.
 __device__ __forceinline__ void dma_step(__amdgpu_buffer_rsrc_t rsw, __amdgpu_buffer_rsrc_t rsa, uint8_t* dst,
-                                         const int* off, const int* chk, int lps, int k0, int K) {
+                                         const int* off, const int* chk, int lps, int k0, int K, int wloads = 2) {
 #pragma unroll
     for (int j = 0; j < lps; ++j) {
         const bool ok = k0 + chk[j] * 16 < K;
-        if (j < 2)                                       // weights, read once: non-temporal
+        if (j < wloads)                                  // weights (the first wloads blocks), read once: non-temporal
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(dst + j * 1024), 16, ok ? off[j] : 0x7fffffff,
                                                      k0, 0, CPOL_NT);
         else
@@ -635,10 +635,11 @@ __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restric
 // ---------------------------------------------------------------------------------------------------------------------
 // out[m, n] = RN_T( fma( sum_k float(w[n, k]) * float(x[m, k]), s[n], bias[n] or +0 ) )   (csrc/w8a16_gemv.cu:98-117,
 // float32 sums; the order of the sum is this kernel's own: the MFMA's and then the 4 K slices in order).
-// The weight stream is the LDS-ring design of stream_lds_kernel (16 weight rows per workgroup, 4 wavefronts on
-// interleaved 128-byte K steps, direct-to-LDS loads of 8 rows x 128 bytes); each 8-byte weight fragment is widened to
-// 8 fp16 / bf16 values in registers and fed to v_mfma_f32_16x16x32_{f16,bf16} as the A operand, the activations
-// (read from L2, 16 bytes per lane) as the B operand.  GATHER: weight rows rows[n] (a gathered vocabulary subset).
+// The weight stream is the LDS-ring design of stream_lds_kernel (RT tiles of 16 weight rows per workgroup, 4
+// wavefronts on interleaved 128-byte K steps, direct-to-LDS loads of 8 rows x 128 bytes); each 8-byte weight fragment
+// is widened to 8 fp16 / bf16 values in registers and fed to v_mfma_f32_16x16x32_{f16,bf16} as the A operand, the
+// activations (read from L2, 16 bytes per lane, once per K step for all RT tiles) as the B operand.  GATHER: weight
+// rows rows[n] (a gathered vocabulary subset).
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bh8 __attribute__((ext_vector_type(8)));
@@ -667,15 +668,15 @@ __device__ __forceinline__ bh8 widen_bf16(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(bh8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <typename T, int MT, int NS, bool GATHER>
+template <typename T, int MT, int NS, bool GATHER, int RT = 1>
 __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
                                                     const float* __restrict__ s, const uint16_t* __restrict__ bias,
                                                     uint16_t* __restrict__ out, int M, int N, int K, int w_rows,
                                                     const int* __restrict__ rows) {
-    constexpr int KS = 4, STEP_BYTES = 16 * 128, LPS = 2;
+    constexpr int KS = 4, STEP_BYTES = RT * 16 * 128, LPS = 2 * RT;   // RT 16-row tiles share each activation load
     extern __shared__ v4i ldsx[];
     const int ks = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * RT;
     uint8_t* const ring = reinterpret_cast<uint8_t*>(ldsx) + ks * NS * STEP_BYTES;
     const __amdgpu_buffer_rsrc_t rsw = make_rsrc(w, (long)w_rows * K);
     int off[LPS], chk[LPS];
@@ -696,7 +697,7 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
     uint4 xr[NS][4][MT];
     auto issue = [&](int i, int slot) {
         const int k0 = (ks + i * KS) * 128;
-        dma_step(rsw, rsw, ring + slot * STEP_BYTES, off, chk, LPS, k0, K);
+        dma_step(rsw, rsw, ring + slot * STEP_BYTES, off, chk, LPS, k0, K, LPS);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -705,26 +706,32 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
                 xr[slot][j][mt] = *reinterpret_cast<const uint4*>(x + (long)m * K + k);
             }
     };
-    f4 acc[MT];
+    f4 acc[RT][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int slot, int k0) {
         const uint8_t* st = ring + slot * STEP_BYTES;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {                    // 32-element MFMA K blocks of the 128-byte step
             const int c = 2 * j + (g >> 1);
-            const uint2 wv = *reinterpret_cast<const uint2*>(st + r * 128 + (c ^ swz<8>(r)) * 16 + 8 * (g & 1));
             const int k = k0 + 32 * j + 8 * g;           // this lane's 8 activations
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int m = mt * 16 + r;
-                const uint4 xv = m < M && k < K ? xr[slot][j][mt] : make_uint4(0, 0, 0, 0);
-                if constexpr (__is_same(T, f16))
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(widen_f16(wv.x, wv.y),
-                                                                     __builtin_bit_cast(h8, xv), acc[mt], 0, 0, 0);
-                else
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(widen_bf16(wv.x, wv.y),
-                                                                      __builtin_bit_cast(bh8, xv), acc[mt], 0, 0, 0);
+            for (int rt = 0; rt < RT; ++rt) {
+                const int wr = rt * 16 + r;              // staged weight row
+                const uint2 wv = *reinterpret_cast<const uint2*>(st + wr * 128 + (c ^ swz<8>(wr)) * 16 + 8 * (g & 1));
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int m = mt * 16 + r;
+                    const uint4 xv = m < M && k < K ? xr[slot][j][mt] : make_uint4(0, 0, 0, 0);
+                    if constexpr (__is_same(T, f16))
+                        acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            widen_f16(wv.x, wv.y), __builtin_bit_cast(h8, xv), acc[rt][mt], 0, 0, 0);
+                    else
+                        acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            widen_bf16(wv.x, wv.y), __builtin_bit_cast(bh8, xv), acc[rt][mt], 0, 0, 0);
+                }
             }
         }
     };
@@ -750,34 +757,42 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
     // K slices meet in LDS, in slice order
     __syncthreads();
     float* red = reinterpret_cast<float*>(ldsx) + lane;
+    constexpr int PER = RT * MT * 4;                     // partial sums per lane
     if (ks > 0) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[((ks - 1) * MT * 4 + mt * 4 + v) * 64] = acc[mt][v];
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    red[((ks - 1) * PER + (rt * MT + mt) * 4 + v) * 64] = acc[rt][mt][v];
     }
     __syncthreads();
     if (ks > 0) return;
 #pragma unroll
     for (int q = 0; q < KS - 1; ++q)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[mt][v] += red[(q * MT * 4 + mt * 4 + v) * 64];
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[rt][mt][v] += red[(q * PER + (rt * MT + mt) * 4 + v) * 64];
     // D of v_mfma_f32_16x16x32: lane holds rows 4 g + v (weight rows) of column r (activation row)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + r;
-        if (m >= M) continue;
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = n0 + 4 * g + v;
-            if (n >= N) continue;
-            const int src = GATHER ? min(max(rows[n], 0), w_rows - 1) : n;
-            const float b = bias ? to_float(T{bias[src]}) : 0.0f;
-            out[(long)m * N + n] = from_float<T>(__builtin_fmaf(acc[mt][v], s[src], b));
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + r;
+            if (m >= M) continue;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = n0 + rt * 16 + 4 * g + v;
+                if (n >= N) continue;
+                const int src = GATHER ? min(max(rows[n], 0), w_rows - 1) : n;
+                const float b = bias ? to_float(T{bias[src]}) : 0.0f;
+                out[(long)m * N + n] = from_float<T>(__builtin_fmaf(acc[rt][mt][v], s[src], b));
+            }
         }
-    }
 }
 
 // w8a16_dot_kernel: M <= 3 rows of the int8 LM head through the VALU.  The weight stream of gemv_dot4_kernel (each
@@ -1251,11 +1266,20 @@ static bool launch_w8a16_dot(const void* x, const void* w, const void* s, const 
     return false;
 }
 
+// Several 16-row weight tiles per workgroup share each activation fragment (the activations are re-read from L2 by
+// every workgroup: at M = 16, 4 KB per 128-byte K step against 2 KB of weights), all weight loads non-temporal.
+// N = 248320, K = 5120, bf16, against one tile: two tiles M=4 251 -> 226 us, M=8 288 -> 240, M=16 378 -> 290, M=32
+// 730 -> 445; three tiles (72 KB rings, two workgroups per CU) M=4 248, M=8 262, M=16 291, M=32 379 us; four tiles
+// (one workgroup per CU) lose at M <= 16.  So two tiles up to M = 16 and three above.
 template <typename T, int MT, bool GATHER>
 static void launch_w8a16_t(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
                            int K, int w_rows, const int* rows, hipStream_t st) {
-    constexpr int NS = 3, LDS = 4 * NS * 16 * 128;
-    w8a16_kernel<T, MT, NS, GATHER><<<(N + 15) / 16, 256, LDS, st>>>(
+    constexpr int NS = 3, RT = MT == 1 ? 2 : 3, LDS = 4 * NS * RT * 16 * 128;
+    static_assert(LDS >= 3 * RT * MT * 4 * 64 * 4, "the K-slice reduction fits in the rings");
+    const void* kern = reinterpret_cast<const void*>(&w8a16_kernel<T, MT, NS, GATHER, RT>);
+    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+    (void)attr;
+    w8a16_kernel<T, MT, NS, GATHER, RT><<<(N + 16 * RT - 1) / (16 * RT), 256, LDS, st>>>(
         static_cast<const uint16_t*>(x), static_cast<const int8_t*>(w), static_cast<const float*>(s),
         static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), M, N, K, w_rows, rows);
 }
