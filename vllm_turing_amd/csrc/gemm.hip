@@ -542,17 +542,18 @@ __device__ __forceinline__ void dma_step(__amdgpu_buffer_rsrc_t rsw, __amdgpu_bu
     }
 }
 
-template <typename T, int MT, int NS, int EPI, int KS = 4>
+template <typename T, int MT, int NS, int EPI, int KS = 4, int RT = 1>
 __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                          const float* __restrict__ sa, const float* __restrict__ sw,
                                                          const uint16_t* __restrict__ bias, void* __restrict__ out,
                                                          int M, int N, int K, int sa_rows, int sw_rows) {
-    constexpr int ROWS = 16 + 16 * MT;                   // staged rows per step
+    constexpr int WR = 16 * RT;                          // weight rows per workgroup (RT tiles of 16)
+    constexpr int ROWS = WR + 16 * MT;                   // staged rows per step: weights, then activations
     constexpr int STEP_BYTES = ROWS * 128;
     constexpr int LPS = ROWS / 8;                        // 1 KB loads per step
     extern __shared__ v4i ldsx[];
     const int ks = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * WR;
     uint8_t* const ring = reinterpret_cast<uint8_t*>(ldsx) + ks * NS * STEP_BYTES;
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
     int off[LPS], chk[LPS];
@@ -560,28 +561,38 @@ __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restric
     for (int j = 0; j < LPS; ++j) {
         const int row = j * 8 + (lane >> 3);             // staged row; lane % 8 is the physical chunk
         chk[j] = (lane & 7) ^ swz<8>(row);
-        if (j < 2) off[j] = n0 + row < N ? (n0 + row) * K + chk[j] * 16 : 0x7fffffff;
-        else off[j] = row - 16 < M ? (row - 16) * K + chk[j] * 16 : 0x7fffffff;
+        if (j < WR / 8) off[j] = n0 + row < N ? (n0 + row) * K + chk[j] * 16 : 0x7fffffff;
+        else off[j] = row - WR < M ? (row - WR) * K + chk[j] * 16 : 0x7fffffff;
     }
     const int nsteps = (K + 127) >> 7;
     const int mine = ks < nsteps ? (nsteps - 1 - ks) / KS + 1 : 0;   // own steps ks, ks + KS, ...
     auto issue = [&](int i) {
-        dma_step(rsw, rsa, ring + (i % NS) * STEP_BYTES, off, chk, LPS, (ks + i * KS) * 128, K);
+        dma_step(rsw, rsa, ring + (i % NS) * STEP_BYTES, off, chk, LPS, (ks + i * KS) * 128, K, WR / 8);
     };
-    v4i acc[MT];
+    v4i acc[RT][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = v4i{0, 0, 0, 0};
     const int r = lane & 15, g = lane >> 4;
     auto compute = [&](int slot) {
         const v4i* st = reinterpret_cast<const v4i*>(ring + slot * STEP_BYTES);
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const int c = 4 * sub + g;                   // this lane's 16-byte chunk of the 128-byte step
-            const v4i fw = st[r * 8 + (c ^ swz<8>(r))];
+            v4i fa[MT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const int ra = 16 + 16 * mt + r;
-                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw, st[ra * 8 + (c ^ swz<8>(ra))], acc[mt], 0, 0, 0);
+                const int ra = WR + 16 * mt + r;
+                fa[mt] = st[ra * 8 + (c ^ swz<8>(ra))];
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int rw = rt * 16 + r;
+                const v4i fw = st[rw * 8 + (c ^ swz<8>(rw))];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[rt][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw, fa[mt], acc[rt][mt], 0, 0, 0);
             }
         }
     };
@@ -603,31 +614,40 @@ __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restric
     // K slices meet in LDS (after every wavefront is done with its ring)
     __syncthreads();
     int* red = reinterpret_cast<int*>(ldsx) + lane;
+    constexpr int PER = RT * MT * 4;                     // partial sums per lane
     if (ks > 0) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[((ks - 1) * MT * 4 + mt * 4 + v) * 64] = acc[mt][v];
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) red[((ks - 1) * PER + (rt * MT + mt) * 4 + v) * 64] = acc[rt][mt][v];
     }
     __syncthreads();
     if (ks > 0) return;
 #pragma unroll
     for (int q = 0; q < KS - 1; ++q)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[mt][v] += red[(q * MT * 4 + mt * 4 + v) * 64];
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[rt][mt][v] += red[(q * PER + (rt * MT + mt) * 4 + v) * 64];
     // D fragment of v_mfma_i32_16x16x64_i8: lane holds rows 4 g + v (weight rows n) of column r (activation row m)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + r;
-        if (m >= M) continue;
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = n0 + 4 * g + v;
-            if (n < N) store_out<T, EPI>(out, (long)m * N + n, acc[mt][v], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0, bias);
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + r;
+            if (m >= M) continue;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = n0 + rt * 16 + 4 * g + v;
+                if (n < N)
+                    store_out<T, EPI>(out, (long)m * N + n, acc[rt][mt][v], sa, sa_rows ? m : 0, sw, sw_rows ? n : 0,
+                                      bias);
+            }
         }
-    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -1015,11 +1035,11 @@ static void launch_dot4(const Args& p) {
 // else a 2-step ring, is used if that fits every tile in one round: K = 5120, N = 17408, M = 8 19.6 -> 18.4 us,
 // M = 16 21.9 -> 20.9 us, M = 32 30.9 -> 27.4 us.  Where four wavefronts already fill their rounds the narrower
 // workgroups are slower (N = 5120, K = 17408, M = 8: 20.4 -> 29.1 us).
-template <typename T, int MT, int NS, int KS, int EPI>
+template <typename T, int MT, int NS, int KS, int EPI, int RT>
 struct SldsCfg {
-    static constexpr int LDS = KS * NS * (16 + 16 * MT) * 128;
-    static_assert(LDS <= 160 * 1024, "LDS ring size");
-    static const void* kern() { return reinterpret_cast<const void*>(&stream_lds_kernel<T, MT, NS, EPI, KS>); }
+    static constexpr int LDS = KS * NS * (16 * RT + 16 * MT) * 128;
+    static_assert(LDS <= 160 * 1024 && LDS >= (KS - 1) * RT * MT * 4 * 64 * 4, "LDS ring size");
+    static const void* kern() { return reinterpret_cast<const void*>(&stream_lds_kernel<T, MT, NS, EPI, KS, RT>); }
     static int slots() {                                 // resident workgroups on the whole GPU
         static const int n = [] {
             (void)hipFuncSetAttribute(kern(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -1032,21 +1052,48 @@ struct SldsCfg {
     static void launch(const Args& p) {
         static const hipError_t attr = hipFuncSetAttribute(kern(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
         (void)attr;
-        stream_lds_kernel<T, MT, NS, EPI, KS><<<(p.N + 15) / 16, 64 * KS, LDS, p.st>>>(
+        stream_lds_kernel<T, MT, NS, EPI, KS, RT><<<(p.N + 16 * RT - 1) / (16 * RT), 64 * KS, LDS, p.st>>>(
             p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows);
     }
 };
+// The configuration of RT tiles per workgroup that the round rule picks, launched if `launch`; returns the fraction
+// of the resident slot-rounds its workgroups fill.
+template <typename T, int MT, int RT, int EPI>
+static double stream_lds_plan(const Args& p, bool launch) {
+    using Wide = SldsCfg<T, MT, 3, 4, EPI, RT>;
+    using Two = SldsCfg<T, MT, 3, 2, EPI, RT>;
+    using TwoShort = SldsCfg<T, MT, 2, 2, EPI, RT>;
+    const int tiles = (p.N + 16 * RT - 1) / (16 * RT), s0 = Wide::slots(), last = tiles % s0;
+    int which = 0, slots = s0;
+    if (tiles > s0 && last > 0 && 2 * last < s0) {
+        if (tiles <= Two::slots()) which = 1, slots = Two::slots();
+        else if (tiles <= TwoShort::slots()) which = 2, slots = TwoShort::slots();
+    }
+    if (launch) {
+        if (which == 1) Two::launch(p);
+        else if (which == 2) TwoShort::launch(p);
+        else Wide::launch(p);
+    }
+    const int rounds = (tiles + slots - 1) / slots;
+    return (double)tiles / ((double)rounds * slots);
+}
+// Above 16 rows the activations are 4 KB per 128-byte K step against 2 KB of weights per 16-row tile, so a workgroup
+// covers up to three tiles that share each activation fragment: of three, two and one tiles per workgroup the launch
+// takes the one whose workgroups fill the most of their slot-rounds (ties to more tiles).  M = 32, K = 5120 against
+// one tile: N = 12288 23.8 -> 17.1 us (three), N = 34816 55.5 -> 46.3 (three), N = 6144 13.2 -> 11.8 (two); N = 5120,
+// K = 17408 34.0 -> 27.0 us (two; three leave 107 workgroups on 256 CUs).  At M <= 16 (2 KB of activations per
+// step) several tiles per workgroup measured slower.
 template <typename T, int MT, int EPI>
 static void launch_stream_lds(const Args& p) {
-    using Wide = SldsCfg<T, MT, 3, 4, EPI>;
-    using Two = SldsCfg<T, MT, 3, 2, EPI>;
-    using TwoShort = SldsCfg<T, MT, 2, 2, EPI>;
-    const int tiles = (p.N + 15) / 16, s0 = Wide::slots(), last = tiles % s0;
-    if (tiles > s0 && last > 0 && 2 * last < s0) {
-        if (tiles <= Two::slots()) return Two::launch(p);
-        if (tiles <= TwoShort::slots()) return TwoShort::launch(p);
+    if constexpr (MT == 1) {
+        stream_lds_plan<T, 1, 1, EPI>(p, true);
+    } else {
+        const double f3 = stream_lds_plan<T, MT, 3, EPI>(p, false), f2 = stream_lds_plan<T, MT, 2, EPI>(p, false),
+                     f1 = stream_lds_plan<T, MT, 1, EPI>(p, false);
+        if (f3 >= f2 && f3 >= f1) stream_lds_plan<T, MT, 3, EPI>(p, true);
+        else if (f2 >= f1) stream_lds_plan<T, MT, 2, EPI>(p, true);
+        else stream_lds_plan<T, MT, 1, EPI>(p, true);
     }
-    Wide::launch(p);
 }
 
 // M <= 32: the VALU kernel where it applies, else the LDS-ring MFMA streaming kernel.
