@@ -63,8 +63,11 @@ def traffic_from_profiles(key):
     return None
 
 
-def graph_time(torch, launch, n_launch_per_graph, steps, warmup):
-    """Capture n launches in a HIP graph, replay; return ms per launch over `steps` launches."""
+def graph_time(torch, launch, n_launch_per_graph, steps, warmup, min_warm_s=0.05):
+    """Capture n launches in a HIP graph, replay; return ms per launch over `steps` launches.  The untimed warm-up
+    replays are at least `warmup` launches and at least `min_warm_s` seconds of GPU work, just before the timed
+    replays (a synchronization between them): after an idle gap (the capture) a GEMM's launches were measured slowing from 224 to 266 us and
+    settling at 218 us only after ~100 launches (the power management's transient), which a short warm-up would time."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -76,13 +79,18 @@ def graph_time(torch, launch, n_launch_per_graph, steps, warmup):
     with torch.cuda.graph(g):
         for i in range(n_launch_per_graph):
             launch(i)
-    reps_w = max(1, warmup // n_launch_per_graph)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()                                       # one replay to size the warm-up
+    e1.record()
+    torch.cuda.synchronize()
+    one_s = max(e0.elapsed_time(e1) * 1e-3, 1e-6)
+    reps_w = max(1, warmup // n_launch_per_graph, int(min_warm_s / one_s + 0.999))
     reps = max(1, (steps + n_launch_per_graph - 1) // n_launch_per_graph)
     for _ in range(reps_w):
         g.replay()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
         g.replay()
