@@ -213,9 +213,10 @@ struct GemmCfg {
     static constexpr int PITCH = WTN * 2 + 8;            // epilogue LDS row: 16-bit outputs + 8 bytes of padding
     static constexpr int EPI_BYTES = WAVES * WTM * PITCH;
     static constexpr int LDS_BYTES = EPI_BYTES > NS * STAGE_BYTES ? EPI_BYTES : NS * STAGE_BYTES;
-    static constexpr int BPW = BM / RPB / WAVES;         // 1 KB blocks per wavefront per operand per stage
-    static constexpr int LPW = 2 * BPW;                  // direct-to-LDS loads per wavefront per stage
-    static_assert(BM == BN && BPW * RPB * WAVES == BM, "A and W stages are filled by the same lanes");
+    static constexpr int BPWA = BM / RPB / WAVES;        // 1 KB blocks of A per wavefront per stage
+    static constexpr int BPWW = BN / RPB / WAVES;        // 1 KB blocks of W per wavefront per stage
+    static constexpr int LPW = BPWA + BPWW;              // direct-to-LDS loads per wavefront per stage
+    static_assert(BPWA * RPB * WAVES == BM && BPWW * RPB * WAVES == BN, "stages split evenly over the wavefronts");
     static_assert(SUPER % BM == 0 && SUPER % BN == 0, "workgroup tiles divide the super tile");
     static_assert(NS >= 2 && NS <= 4 && LDS_BYTES <= 160 * 1024, "stage configuration");
 };
@@ -356,27 +357,32 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
 
 constexpr int CPOL_NT = 2;                                // cache-policy operand of a buffer load: non-temporal
 
-// One K stage of a wavefront's share of A and W (bpw 1 KB blocks of each), straight into LDS.  Block j's lane reads
-// logical chunk ch[j] of its row at offset o*[j]; chunks past the end of K get an offset outside the buffer, which
-// makes the load write zeros.  A plain device function (bpw is a constant after inlining): in a template context the
-// host pass treats the buffer-descriptor type as a substitution failure and silently drops the kernel's host stub.
+// Part of one K stage of a wavefront's share of A and W, straight into LDS: its A blocks ja0..ja1 - 1 and W blocks
+// jw0..jw1 - 1 (of bpwa and bpww 1 KB blocks per stage), issued alternately.  Block j's lane reads logical chunk ch*[j]
+// of its row at offset o*[j]; chunks past the end of K get an offset outside the buffer, which makes the load write
+// zeros.  A plain device function (the ranges are constants after inlining): in a template context the host pass
+// treats the buffer-descriptor type as a substitution failure and silently drops the kernel's host stub.
 __device__ __forceinline__ void dma_part(__amdgpu_buffer_rsrc_t rsa, __amdgpu_buffer_rsrc_t rsw, uint8_t* stage_l,
-                                         int a_bytes, const int* oa, const int* ow, const int* ch, int bpw, int j0,
-                                         int j1, int k0, int K, int wave) {
+                                         int a_bytes, const int* oa, const int* cha, int bpwa, int ja0, int ja1,
+                                         const int* ow, const int* chw, int bpww, int jw0, int jw1, int k0, int K,
+                                         int wave) {
     uint8_t* sa_l = stage_l;
     uint8_t* sw_l = stage_l + a_bytes;
+    const int n = max(ja1 - ja0, jw1 - jw0);
 #pragma unroll
-    for (int j = j0; j < j1; ++j) {
-        const int blk = (wave * bpw + j) * 1024;
-        const bool ok = k0 + ch[j] * 16 < K;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sa_l + blk), 16, ok ? oa[j] : 0x7fffffff, k0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sw_l + blk), 16, ok ? ow[j] : 0x7fffffff, k0, 0, 0);
+    for (int i = 0; i < n; ++i) {
+        const int ja = ja0 + i, jw = jw0 + i;
+        if (ja < ja1) {
+            const bool ok = k0 + cha[ja] * 16 < K;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sa_l + (wave * bpwa + ja) * 1024), 16,
+                                                     ok ? oa[ja] : 0x7fffffff, k0, 0, 0);
+        }
+        if (jw < jw1) {
+            const bool ok = k0 + chw[jw] * 16 < K;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sw_l + (wave * bpww + jw) * 1024), 16,
+                                                     ok ? ow[jw] : 0x7fffffff, k0, 0, 0);
+        }
     }
-}
-__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rsa, __amdgpu_buffer_rsrc_t rsw, uint8_t* stage_l,
-                                          int a_bytes, const int* oa, const int* ow, const int* ch, int bpw, int k0,
-                                          int K, int wave) {
-    dma_part(rsa, rsw, stage_l, a_bytes, oa, ow, ch, bpw, 0, bpw, k0, K, wave);
 }
 
 
@@ -416,24 +422,32 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
     // stage s is computed, so no register holds staged data and the memory latency has NS - 1 stages of MFMA
     // work to hide behind.
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
-    constexpr int CPR = Cfg::CPR, BPW = Cfg::BPW;
+    constexpr int CPR = Cfg::CPR, BPWA = Cfg::BPWA, BPWW = Cfg::BPWW;
     const int drow = lane / CPR, pch = lane % CPR;       // row within the 1 KB block; physical chunk position
-    int oa[BPW], ow[BPW], ch[BPW];
+    int oa[BPWA], cha[BPWA], ow[BPWW], chw[BPWW];        // ch*: the logical chunk the swizzle stores at this position
 #pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-        const int row = (wave * BPW + j) * Cfg::RPB + drow;
-        ch[j] = pch ^ swz<CPR>(row);                     // the logical chunk the swizzle stores at this position
-        oa[j] = min(m0 + row, M - 1) * K + ch[j] * 16;
-        ow[j] = min(n0 + row, N - 1) * K + ch[j] * 16;
+    for (int j = 0; j < BPWA; ++j) {
+        const int row = (wave * BPWA + j) * Cfg::RPB + drow;
+        cha[j] = pch ^ swz<CPR>(row);
+        oa[j] = min(m0 + row, M - 1) * K + cha[j] * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < BPWW; ++j) {
+        const int row = (wave * BPWW + j) * Cfg::RPB + drow;
+        chw[j] = pch ^ swz<CPR>(row);
+        ow[j] = min(n0 + row, N - 1) * K + chw[j] * 16;
     }
     uint8_t* const lbase = reinterpret_cast<uint8_t*>(ldsx);
     auto issue = [&](int stage, int k0) {
-        dma_stage(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, ow, ch, BPW, k0, K, wave);
+        dma_part(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, cha, BPWA, 0, BPWA, ow, chw, BPWW, 0, BPWW,
+                 k0, K, wave);
     };
-    auto issue_part = [&](int stage, int k0, int j0, int j1) {
-        dma_part(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, ow, ch, BPW, j0, j1, k0, K, wave);
+    auto issue_slice = [&](int stage, int k0, int sl) {  // slice sl of SPLIT
+        dma_part(rsa, rsw, lbase + stage * Cfg::STAGE_BYTES, BM * KB, oa, cha, BPWA, sl * BPWA / SPLIT,
+                 (sl + 1) * BPWA / SPLIT, ow, chw, BPWW, sl * BPWW / SPLIT, (sl + 1) * BPWW / SPLIT, k0, K, wave);
     };
-    static_assert(SPLIT == 0 || (BPW % SPLIT == 0 && SPLIT <= KB / 32 + (LEAD ? 1 : 0)), "DMA slices");
+    static_assert(SPLIT == 0 || (BPWA % SPLIT == 0 && BPWW % SPLIT == 0 && SPLIT <= KB / 32 + (LEAD ? 1 : 0)),
+                  "DMA slices");
 
     const int wm = wave / WN, wn = wave % WN;
     v16i acc[FM][FN];
@@ -481,7 +495,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (SPLIT > 0) {                       // next-stage slice sl after this sub-step's MFMAs
                 const int sl = sub + (LEAD ? 1 : 0);
-                if (sl < SPLIT && nk0 >= 0) issue_part(nstage, nk0, sl * BPW / SPLIT, (sl + 1) * BPW / SPLIT);
+                if (sl < SPLIT && nk0 >= 0) issue_slice(nstage, nk0, sl);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -503,7 +517,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
         __builtin_amdgcn_s_barrier();
         const bool more = kt + NS - 1 < nk;
         if (SPLIT == 0 && more) issue((kt + NS - 1) % NS, (kt + NS - 1) * KB);
-        if (SPLIT > 0 && LEAD && more) issue_part((kt + NS - 1) % NS, (kt + NS - 1) * KB, 0, BPW / SPLIT);
+        if (SPLIT > 0 && LEAD && more) issue_slice((kt + NS - 1) % NS, (kt + NS - 1) * KB, 0);
         compute(kt % NS, (kt + NS - 1) % NS, more ? (kt + NS - 1) * KB : -1);
     }
 
@@ -1126,6 +1140,12 @@ struct SmallCfg {
     static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128, NS = 2, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
+// Tiny configuration: 64 x 128 eighth tiles, 2 x 2 wavefronts of 32 x 64 (48 KB: three workgroups per CU), for a last
+// round of so few super tiles that the quarter tiles would put two workgroups on some CUs and one on others.
+struct TinyCfg {
+    static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 2, SPLIT = 0;
+    static constexpr bool LEAD = false;
+};
 constexpr int LONG_ROUNDS = 6;
 
 // Which configuration covers which super tiles: 0 = main only, 2 = small only, 1 = main for the whole rounds of super
@@ -1167,7 +1187,12 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
     }
     if (full > 0 && longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, full);
     else if (full > 0) launch_gemm_cfg<T, EPI, MainCfg>(p, 0, full);
-    launch_gemm_cfg<T, EPI, SmallCfg>(p, full, rem * SUB);
+    // the remainder as quarter tiles, or as eighth tiles where the quarters would leave at least half the CUs idle:
+    // M = 512, N = 34816 (16 remaining super tiles) 106.2 -> 100.2 us; where the quarters already cover the CUs the
+    // eighth tiles' extra fragment reads cost more than their balance gains (M = 512, N = 12288: 40.4 -> 45.7 us)
+    constexpr int SUBT = GemmCfg<TinyCfg::WM, TinyCfg::WN, TinyCfg::FM, TinyCfg::FN, TinyCfg::KB, TinyCfg::NS>::SUB;
+    if (2 * rem * SUB <= cus) launch_gemm_cfg<T, EPI, TinyCfg>(p, full, rem * SUBT);
+    else launch_gemm_cfg<T, EPI, SmallCfg>(p, full, rem * SUB);
 }
 
 template <int EPI>
