@@ -8,7 +8,8 @@ stream from HBM.  Launches are captured in a HIP graph of 20 back-to-back launch
 is GPU work only (HIP events on the launch stream, bracketed by synchronizations).
 
 Also reported:
-  decode_other_m: the same GEMV at M = 2, 4, 8;
+  decode_other_m: the same weights at M = 2, 4, 8, 16, 32, 64 through the entry the reference dispatches at that M
+    (GEMV up to 12 rows, the mid-band MMA up to 32, the large-M GEMM above);
   gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, in TOPS of 2*M*N*K ops (MFMA-bound roofline),
     timed after a 2 s untimed run of it that samples the median gfx clock amd-smi reports (sclk_mhz) and settles
     the clock, with the fraction of the peak scaled to that clock (frac_at_sclk; the 5.0 POP/s peak is quoted at
@@ -381,22 +382,30 @@ def bench_headline(torch, L, st, dev, args):
 
     # the other decode batch sizes of the same projection (M = 2, 4, 8), same weights and method
     decode_m = {}
-    for Md in (2, 4, 8):
+    for Md in (2, 4, 8, 16, 32, 64):
         cd = workloads.decode(Md)
         xq_d, xs_d = per_token_quant(cd["x"].to(dev))
         out_d = torch.empty(Md, N, dtype=torch.float16, device=dev)
 
         def gemv_d(i, Md=Md, xq_d=xq_d, xs_d=xs_d, out_d=out_d):
-            rc = L.w8a8_gemv(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(), None,
-                             out_d.data_ptr(), Md, N, K, 1, 1, 0, st())
+            # the entry the reference's dispatch takes at this M (w8a8.py:108-117): GEMV, mid-band MMA, big GEMM
+            if Md <= 12:
+                rc = L.w8a8_gemv(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(), None,
+                                 out_d.data_ptr(), Md, N, K, 1, 1, 0, st())
+            elif Md <= 32:
+                rc = L.w8a8_mma(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(), None,
+                                out_d.data_ptr(), Md, N, K, 1, 1, 0, st())
+            else:
+                rc = L.w8a8_big(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(),
+                                out_d.data_ptr(), Md, N, K, 0, st())
             if rc != 0:
-                raise RuntimeError(f"w8a8_gemv {rc}")
+                raise RuntimeError(f"decode M={Md}: {rc}")
 
         ms_d, _ = graph_time(torch, gemv_d, 4 * copies, 400, 40)
         b_d = N * K + Md * K + 2 * Md * N + 4 * N + 4 * Md
         decode_m[f"M{Md}"] = {"us": round(ms_d * 1e3, 2), "gbs": round(b_d / ms_d / 1e6, 1),
                               "frac": round(b_d / ms_d / 1e6 / HBM_PEAK_GBS, 4)}
-    print(f"[bench] GEMV M=2/4/8: {decode_m}", file=sys.stderr, flush=True)
+    print(f"[bench] GEMV M=2..64: {decode_m}", file=sys.stderr, flush=True)
     del ws
 
     # ---- prefill GEMM, M=4096, bias, bf16 ---------------------------------------------------------------------------
@@ -534,7 +543,8 @@ def bench_headline(torch, L, st, dev, args):
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_m1")},
         "cpu_baseline": cpu,
-        "decode_other_m": {"workload": f"decode W8A8 GEMV K={K} N={N}, fp16 out, same weights and method",
+        "decode_other_m": {"workload": f"decode W8A8 K={K} N={N}, fp16 out, same rotated weights, the entry the reference "
+                                       f"dispatches at each M (w8a8_gemv <= 12, w8a8_mma <= 32, w8a8_big above)",
                            **decode_m},
         "gemm": {"workload": f"prefill W8A8 GEMM M={Mg} K={Kg} N={Ng}, bias, bf16 out", "ms": round(ms_gemm, 4),
                  "launches": n_gemm, "tops": round(gemm_tops, 1),

@@ -92,7 +92,7 @@ int w8a16_gemv_rows(const void* x, const void* w, const void* s, const void* bia
                     int dtype, const void* rows, int w_rows, void* stream);
 
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
- * checks: kernel 0 the small-M MFMA streaming kernel (M <= 32), 1 the prefill kernel as dispatched, 2 the v_dot4
+ * checks: kernel 0 the small-M MFMA streaming kernel (M <= 64), 1 the prefill kernel as dispatched, 2 the v_dot4
  * streaming kernel (M = 1 and K <= 17408, M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120), 3 and 4 the prefill
  * kernel's quarter-tile and full-tile configurations alone.  No counterpart in the reference.  Returns -1 on bad
  * arguments, else the HIP launch error. */

@@ -57,7 +57,7 @@ def test_argument_validation_codes(L):
     assert L.w8a8_big(16, 16, 0, 0, 0, 64, 24, 64, 0, None) == 1                  # N % 16
     assert L.w8a8_big(16, 16, 0, 0, 0, 64, 64, 72, 0, None) == 1                  # K % 16
     assert L.w8a8_scaled_mm(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
-    assert L.w8a8_i32(16, 16, 0, 33, 64, 64, 0, None) == -1                       # streaming kernel: M <= 32
+    assert L.w8a8_i32(16, 16, 0, 65, 64, 64, 0, None) == -1                       # streaming kernel: M <= 64
     assert L.w8a8_i32(16, 16, 0, 6, 64, 64, 2, None) == -1                       # VALU kernel: M <= 5
     assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # K <= 17408 at one row
     assert L.w8a8_i32(16, 16, 0, 2, 64, 8208, 2, None) == -1                     # K <= 8192 at two rows

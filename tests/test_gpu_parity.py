@@ -430,7 +430,9 @@ STREAM_SHAPES = [(1, 64, 128), (1, 17408, 5120), (2, 1000, 5136), (3, 300, 5168)
                  (31, 8, 48), (1, 5120, 17408), (4, 5120, 6144), (4, 16384, 5120),
                  # tile counts whose last round of four-wavefront workgroups would be under half full: two-wavefront
                  # workgroups with 3- or 2-step rings, short and ragged K (one wavefront with no K step at K = 16)
-                 (12, 13312, 272), (24, 17408, 1040), (9, 13328, 16), (17, 13312, 5136)]
+                 (12, 13312, 272), (24, 17408, 1040), (9, 13328, 16), (17, 13312, 5136),
+                 # 33..64 rows: four 16-row activation tiles per step
+                 (33, 1000, 5136), (64, 5120, 2048), (48, 17408, 1040), (40, 12288, 272)]
 
 
 @pytest.mark.parametrize("M,N,K", STREAM_SHAPES)
@@ -462,7 +464,9 @@ def test_i32_dot4_kernel(L, M, N, K):
 
 
 GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80), (97, 272, 5120),
-               (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248), (4096, 256, 17408)]
+               (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248), (4096, 256, 17408),
+               # 33..128 rows: streaming passes (small N) or the 4-stage mid configuration (N up to 20480)
+               (100, 12288, 272), (40, 13312, 1040), (128, 9000, 5136), (65, 20480, 144)]
 
 
 # prefill kernel as dispatched (1), its small configuration alone (3) and its main configuration alone (4); the
@@ -541,6 +545,8 @@ CASES = [
     (100, 1000, 5120, torch.float16, False, True, 1),      # per-tensor sa -> general entry
     (4096, 5120, 512, torch.bfloat16, True, False, 1),     # 320 super tiles: main + small launches, bias
     (4160, 5136, 272, torch.float16, False, False, 1),     # ragged edges in both configurations
+    (96, 10240, 1040, torch.bfloat16, True, False, 1),     # mid configuration, bias
+    (70, 5120, 2064, torch.float16, True, True, 1),        # streaming passes (64 + 6 rows), bias, per-tensor sa
 ]
 
 

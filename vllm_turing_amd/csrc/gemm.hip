@@ -218,7 +218,7 @@ struct GemmCfg {
     static constexpr int LPW = BPWA + BPWW;              // direct-to-LDS loads per wavefront per stage
     static_assert(BPWA * RPB * WAVES == BM && BPWW * RPB * WAVES == BN, "stages split evenly over the wavefronts");
     static_assert(SUPER % BM == 0 && SUPER % BN == 0, "workgroup tiles divide the super tile");
-    static_assert(NS >= 2 && NS <= 4 && LDS_BYTES <= 160 * 1024, "stage configuration");
+    static_assert(NS >= 2 && NS <= 6 && LDS_BYTES <= 160 * 1024, "stage configuration");
 };
 
 // 16-byte chunk c of a staged LDS row lives at chunk position c ^ swz(row).  A ds_read_b128 phase serves 8 rows
@@ -501,7 +501,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
         }
     };
 
+    constexpr int WAIT4 = waitcnt_vm(4 * Cfg::LPW), WAIT3 = waitcnt_vm(3 * Cfg::LPW);
     constexpr int WAIT2 = waitcnt_vm(2 * Cfg::LPW), WAIT1 = waitcnt_vm(Cfg::LPW), WAIT0 = waitcnt_vm(0);
+    static_assert(4 * Cfg::LPW <= 63, "vmcnt range");
     const int nk = (K + KB - 1) / KB;
 #pragma unroll
     for (int s0 = 0; s0 < NS - 1; ++s0)
@@ -509,7 +511,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
     for (int kt = 0; kt < nk; ++kt) {
         // this wavefront's loads of stage kt are done once at most the later stages' loads (LPW each) remain
         const int ahead = min(nk - 1 - kt, NS - 2);
-        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
+        if (NS > 5 && ahead >= 4) __builtin_amdgcn_s_waitcnt(WAIT4);
+        else if (NS > 4 && ahead == 3) __builtin_amdgcn_s_waitcnt(WAIT3);
+        else if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAIT2);
         else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAIT1);
         else __builtin_amdgcn_s_waitcnt(WAIT0);
         // every wavefront's part of stage kt is in LDS (each waited for its own loads above).  A bare s_barrier:
@@ -1101,11 +1105,15 @@ template <typename T, int MT, int EPI>
 static void launch_stream_lds(const Args& p) {
     if constexpr (MT == 1) {
         stream_lds_plan<T, 1, 1, EPI>(p, true);
-    } else {
+    } else if constexpr (MT == 2) {
         const double f3 = stream_lds_plan<T, MT, 3, EPI>(p, false), f2 = stream_lds_plan<T, MT, 2, EPI>(p, false),
                      f1 = stream_lds_plan<T, MT, 1, EPI>(p, false);
         if (f3 >= f2 && f3 >= f1) stream_lds_plan<T, MT, 3, EPI>(p, true);
         else if (f2 >= f1) stream_lds_plan<T, MT, 2, EPI>(p, true);
+        else stream_lds_plan<T, MT, 1, EPI>(p, true);
+    } else {                                             // 64 activation rows: three tiles' rings would not fit
+        const double f2 = stream_lds_plan<T, MT, 2, EPI>(p, false), f1 = stream_lds_plan<T, MT, 1, EPI>(p, false);
+        if (f2 >= f1) stream_lds_plan<T, MT, 2, EPI>(p, true);
         else stream_lds_plan<T, MT, 1, EPI>(p, true);
     }
 }
@@ -1146,6 +1154,16 @@ struct TinyCfg {
     static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 2, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
+// Mid configuration: the tiny tiles with 4 K stages in LDS (96 KB, one workgroup per CU) for 33..128 rows, where a
+// tile row holds all of M and each workgroup streams its 128 weight rows with three stages in flight instead of one:
+// K = 5120, N = 12288, M = 96 47.7 -> 25.7 us, M = 128 49.4 -> 27.5; N = 10240, M = 128 49.1 -> 26.8; N = 17408,
+// M = 33 47.2 -> 44.4, M = 128 59.5 -> 47.5 us.  Three stages gain less, six no more; from N = 24576 on the other
+// configurations are as fast or faster (N = 34816, M = 48: 71.3 against 74.3 us).
+struct MidCfg {
+    static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 4, SPLIT = 0;
+    static constexpr bool LEAD = false;
+};
+constexpr int MID_GEMM_MAX_M = 128, MID_GEMM_MAX_N = 20480;
 constexpr int LONG_ROUNDS = 6;
 
 // Which configuration covers which super tiles: 0 = main only, 2 = small only, 1 = main for the whole rounds of super
@@ -1169,9 +1187,41 @@ static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
 }
 
 
+// Up to 64 rows against at most 12288 weight rows, or up to 128 rows against at most 8192: the prefill kernel has
+// few tiles to spread there (N = 5120: 20 super tiles in a single tile row), so the streaming kernel runs instead, in
+// passes of at most 64 rows, with the same epilogue (bit-identical).  Rotated weights, bf16, against the prefill
+// kernel: N = 5120, K = 17408, M = 33..64 114 -> 35-38 us, M = 96 113 -> 65 us, M = 128 114 -> 76 us; N = 12288,
+// K = 5120, M = 33..64 42-45 -> 31-35 us; N = 8192, M = 128 38 -> 36 us.  Past these bounds the prefill kernel is
+// faster (N = 12288, M = 128: 50 against 69 us; N = 17408, M = 33: 46 against 51 us): the passes re-read the weights
+// and the 64-row rings leave few wavefronts per CU.
+static bool mid_stream(int M, int N) { return (M <= 64 && N <= 12288) || (M <= 128 && N <= 8192); }
+template <typename T, int EPI>
+static void launch_stream_rows(const Args& p) {
+    const int esz = EPI == EPI_I32 ? 4 : 2;              // output element bytes
+    for (int m0 = 0; m0 < p.M; m0 += 64) {
+        Args q = p;
+        q.M = min(64, p.M - m0);
+        q.a = p.a + (long)m0 * p.K;
+        q.out = static_cast<uint8_t*>(p.out) + (long)m0 * p.N * esz;
+        if (p.sa_rows) q.sa = p.sa + m0;
+        if (q.M <= 16) launch_stream_lds<T, 1, EPI>(q);
+        else if (q.M <= 32) launch_stream_lds<T, 2, EPI>(q);
+        else launch_stream_lds<T, 4, EPI>(q);
+    }
+}
+
 template <typename T, int EPI>
 static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
+    if (policy == 1 && mid_stream(p.M, p.N)) {
+        launch_stream_rows<T, EPI>(p);
+        return;
+    }
     const int tiles = ((p.M + SUPER - 1) / SUPER) * ((p.N + SUPER - 1) / SUPER);
+    if (policy == 1 && p.M <= MID_GEMM_MAX_M && p.N <= MID_GEMM_MAX_N) {
+        constexpr int SUBM = GemmCfg<MidCfg::WM, MidCfg::WN, MidCfg::FM, MidCfg::FN, MidCfg::KB, MidCfg::NS>::SUB;
+        launch_gemm_cfg<T, EPI, MidCfg>(p, 0, tiles * SUBM);
+        return;
+    }
     constexpr int SUB = GemmCfg<SmallCfg::WM, SmallCfg::WN, SmallCfg::FM, SmallCfg::FN, SmallCfg::KB, SmallCfg::NS>::SUB;
     if (policy == 2) {
         launch_gemm_cfg<T, EPI, SmallCfg>(p, 0, tiles * SUB);
@@ -1272,17 +1322,18 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 }
 
 // Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
-// M <= 32; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M = 1 and K <= 17408 or
-// M = 2 and K <= 8192; kernel 3 = the prefill kernel's small configuration alone; kernel 4 = its main configuration
-// alone).  Returns -1 on bad arguments, else the launch error.
+// M <= 64; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M = 1 and K <= 17408,
+// M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120; kernel 3 = the prefill kernel's quarter-tile configuration alone;
+// kernel 4 = its full-tile configuration alone).  Returns -1 on bad arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
     if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 4) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
                  (hipStream_t)stream};
     if (kernel == 0) {
-        if (M > 32) return -1;
+        if (M > 64) return -1;
         if (M <= 16) launch_stream_lds<f16, 1, EPI_I32>(p);
-        else launch_stream_lds<f16, 2, EPI_I32>(p);
+        else if (M <= 32) launch_stream_lds<f16, 2, EPI_I32>(p);
+        else launch_stream_lds<f16, 4, EPI_I32>(p);
     } else if (kernel == 1) {
         launch_gemm<f16, EPI_I32>(p);
     } else if (kernel == 3) {
