@@ -1154,16 +1154,22 @@ struct TinyCfg {
     static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 2, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
-// Mid configuration: the tiny tiles with 4 K stages in LDS (96 KB, one workgroup per CU) for 33..128 rows, where a
-// tile row holds all of M and each workgroup streams its 128 weight rows with three stages in flight instead of one:
-// K = 5120, N = 12288, M = 96 47.7 -> 25.7 us, M = 128 49.4 -> 27.5; N = 10240, M = 128 49.1 -> 26.8; N = 17408,
-// M = 33 47.2 -> 44.4, M = 128 59.5 -> 47.5 us.  Three stages gain less, six no more; from N = 24576 on the other
-// configurations are as fast or faster (N = 34816, M = 48: 71.3 against 74.3 us).
+// Mid configurations for 33..128 rows, where a tile row holds all of M: 64-row tiles with 4 K stages in LDS, so that
+// each workgroup has three stages of its weight rows in flight instead of one.  Up to N = 12288: 64 x 128 tiles (96
+// KB, one workgroup per CU): K = 5120, N = 12288, M = 96 47.7 -> 25.7 us, M = 128 49.4 -> 27.5; N = 10240, M = 128
+// 49.1 -> 26.8 us.  Above: 64 x 64 tiles (2 x 2 wavefronts of 32 x 32, 64 KB, two workgroups per CU), twice as many
+// workgroups on the weight stream: N = 17408, M = 33 44.1 -> 29.2 us, M = 64 49.1 -> 34.4, M = 128 47.9 -> 42.1;
+// N = 24576, M = 64 53.0 -> 36.5; N = 34816, M = 48 70.7 -> 48.7, M = 128 74.6 -> 70.2 us (at N = 12288, M = 128 the
+// 64 x 64 tiles take 30.5 us against 26.8).  Three stages gained less, six no more.
 struct MidCfg {
     static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 4, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
-constexpr int MID_GEMM_MAX_M = 128, MID_GEMM_MAX_N = 20480;
+struct Mid64Cfg {
+    static constexpr int WM = 2, WN = 2, FM = 1, FN = 1, KB = 128, NS = 4, SPLIT = 0;
+    static constexpr bool LEAD = false;
+};
+constexpr int MID_GEMM_MAX_M = 128, MID_GEMM_WIDE_N = 12288;
 constexpr int LONG_ROUNDS = 6;
 
 // Which configuration covers which super tiles: 0 = main only, 2 = small only, 1 = main for the whole rounds of super
@@ -1217,9 +1223,15 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
         return;
     }
     const int tiles = ((p.M + SUPER - 1) / SUPER) * ((p.N + SUPER - 1) / SUPER);
-    if (policy == 1 && p.M <= MID_GEMM_MAX_M && p.N <= MID_GEMM_MAX_N) {
-        constexpr int SUBM = GemmCfg<MidCfg::WM, MidCfg::WN, MidCfg::FM, MidCfg::FN, MidCfg::KB, MidCfg::NS>::SUB;
-        launch_gemm_cfg<T, EPI, MidCfg>(p, 0, tiles * SUBM);
+    if (policy == 1 && p.M <= MID_GEMM_MAX_M) {
+        if (p.N <= MID_GEMM_WIDE_N) {
+            constexpr int SUBM = GemmCfg<MidCfg::WM, MidCfg::WN, MidCfg::FM, MidCfg::FN, MidCfg::KB, MidCfg::NS>::SUB;
+            launch_gemm_cfg<T, EPI, MidCfg>(p, 0, tiles * SUBM);
+        } else {
+            constexpr int SUB6 =
+                GemmCfg<Mid64Cfg::WM, Mid64Cfg::WN, Mid64Cfg::FM, Mid64Cfg::FN, Mid64Cfg::KB, Mid64Cfg::NS>::SUB;
+            launch_gemm_cfg<T, EPI, Mid64Cfg>(p, 0, tiles * SUB6);
+        }
         return;
     }
     constexpr int SUB = GemmCfg<SmallCfg::WM, SmallCfg::WN, SmallCfg::FM, SmallCfg::FN, SmallCfg::KB, SmallCfg::NS>::SUB;
