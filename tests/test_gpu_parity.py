@@ -467,7 +467,7 @@ GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80
                (1024, 768, 1024), (260, 12288, 128), (64, 512, 17408), (513, 256, 5248), (4096, 256, 17408),
                # 33..128 rows: streaming passes (small N), the 4-stage 64 x 128 (N up to 12288) or 64 x 64 tiles
                (100, 12288, 272), (40, 13312, 1040), (128, 9000, 5136), (65, 20480, 144), (50, 17000, 272),
-               (128, 34816, 48)]
+               (128, 34816, 48), (200, 5120, 1040), (256, 8192, 272)]
 
 
 # prefill kernel as dispatched (1), its small configuration alone (3) and its main configuration alone (4); the

@@ -1160,7 +1160,9 @@ struct TinyCfg {
 // 49.1 -> 26.8 us.  Above: 64 x 64 tiles (2 x 2 wavefronts of 32 x 32, 64 KB, two workgroups per CU), twice as many
 // workgroups on the weight stream: N = 17408, M = 33 44.1 -> 29.2 us, M = 64 49.1 -> 34.4, M = 128 47.9 -> 42.1;
 // N = 24576, M = 64 53.0 -> 36.5; N = 34816, M = 48 70.7 -> 48.7, M = 128 74.6 -> 70.2 us (at N = 12288, M = 128 the
-// 64 x 64 tiles take 30.5 us against 26.8).  Three stages gained less, six no more.
+// 64 x 64 tiles take 30.5 us against 26.8).  Three stages gained less, six no more.  The 64 x 128 tiles also serve
+// 129..256 rows against at most 8192 weight rows, where the other configurations have few tiles to spread: N = 5120,
+// K = 17408, M = 256 111.8 -> 64.4 us; N = 6144, K = 5120, M = 256 37.0 -> 24.4 us (from N = 12288 on they lose).
 struct MidCfg {
     static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 4, SPLIT = 0;
     static constexpr bool LEAD = false;
@@ -1223,7 +1225,7 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
         return;
     }
     const int tiles = ((p.M + SUPER - 1) / SUPER) * ((p.N + SUPER - 1) / SUPER);
-    if (policy == 1 && p.M <= MID_GEMM_MAX_M) {
+    if (policy == 1 && (p.M <= MID_GEMM_MAX_M || (p.M <= 2 * MID_GEMM_MAX_M && p.N <= 8192))) {
         if (p.N <= MID_GEMM_WIDE_N) {
             constexpr int SUBM = GemmCfg<MidCfg::WM, MidCfg::WN, MidCfg::FM, MidCfg::FN, MidCfg::KB, MidCfg::NS>::SUB;
             launch_gemm_cfg<T, EPI, MidCfg>(p, 0, tiles * SUBM);
