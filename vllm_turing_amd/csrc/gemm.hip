@@ -11,24 +11,29 @@
 //    through the VALU: each wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against
 //    activations held in registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain
 //    (csrc/w8a8_gemv.cu:91).
-//  * stream_lds_kernel, the rest of M <= 32 (decode, speculative verify): weight-streaming and HBM-bound.  A workgroup
-//    owns 16 weight rows; its 4 wavefronts take interleaved 128-byte K steps, each through a private LDS ring filled
-//    by direct-to-LDS loads of 1 KB (8 rows x 128 contiguous bytes each), and feed v_mfma_i32_16x16x64_i8 with the
-//    weights as the A operand and up to 16 activation rows per MFMA as the B operand.  The K slices of a tile meet in
-//    LDS.  Small-M epilogue chain.
+//  * stream_lds_kernel, the rest of M <= 32 (decode, speculative verify), and passes of up to 64 rows for 33..128 rows
+//    against small N: weight-streaming and HBM-bound.  A workgroup owns one to three 16-row weight tiles; its 4 (or 2)
+//    wavefronts take interleaved 128-byte K steps, each through a private LDS ring filled by direct-to-LDS loads of
+//    1 KB (8 rows x 128 contiguous bytes each), and feed v_mfma_i32_16x16x64_i8 with the weights as the A operand and
+//    up to 16 activation rows per MFMA as the B operand.  The K slices of a tile meet in LDS.  The launch picks the
+//    wavefronts, ring depth and tiles per workgroup from how the tiles fill the resident slots.  Small-M epilogue
+//    chain (the large-M one when it serves the prefill entry).
 //  * w8a16_dot_kernel (the int8 LM head: fp16 / bf16 activations, M <= 3): the dot4 kernel's weight stream, each
 //    weight widened exactly to 16-bit pairs for v_dot2_f32_{f16,bf16}; float32 sums.
-//  * w8a16_kernel (the int8 LM head, the rest of M <= 32): the LDS-ring weight stream with each int8 fragment
-//    widened to fp16 / bf16 in registers for v_mfma_f32_16x16x32_{f16,bf16}; float32 sums.
+//  * w8a16_kernel (the int8 LM head, the rest of M <= 32): the LDS-ring weight stream (two or three 16-row tiles per
+//    workgroup sharing each activation fragment) with each int8 fragment widened to fp16 / bf16 in registers for
+//    v_mfma_f32_16x16x32_{f16,bf16}; float32 sums.
 //  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
 //    each a 4 x 2 grid of v_mfma_i32_32x32x32_i8; 128-byte K stages loaded straight from HBM into LDS
 //    (buffer_load ... lds), double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128
 //    conflict-free, and the operand fragments of the next 32-byte sub-step read from LDS during the current one's
 //    MFMAs; workgroups remapped so the tiles resident on one XCD share A rows and W rows in that XCD's L2.  Where the
 //    tiles leave a last partial round over the CUs, that round runs as 128 x 128 quarter tiles (4 wavefronts of
-//    64 x 64, two workgroups per CU) so it spreads over the whole chip.  The next stage's loads go out in slices
-//    between the MFMA blocks of the first sub-steps.  The epilogue goes through LDS so that every global store writes
-//    whole lines, non-temporally.  Large-M epilogue (csrc/w8a8_big.cu:26-35).
+//    64 x 64, two workgroups per CU), or 64 x 128 eighth tiles where the quarters would leave half the CUs idle, so
+//    it spreads over the whole chip.  33..128 rows (and 129..256 against small N) run on 64 x 128 or 64 x 64 tiles
+//    with 4 K stages in flight.  The next stage's loads go out in slices between the MFMA blocks of the first
+//    sub-steps.  The epilogue goes through LDS so that every global store writes whole lines, non-temporally.
+//    Large-M epilogue (csrc/w8a8_big.cu:26-35).
 //
 // The kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
 // MFMA the same permutation of k on its A and B operands (the dot4 kernel pairs weight and activation chunks the
