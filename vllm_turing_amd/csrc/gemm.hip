@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
             // fences keep the next sub-step's fragment reads ahead of this sub-step's MFMAs (left alone, the
             // scheduler re-reads each fragment just before its MFMAs and exposes the LDS latency every time)
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);   // favour the wavefront issuing MFMAs (measured neutral)
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);   // favour the MFMA-issuing wavefront (measured neutral)
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -861,8 +861,10 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 __device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, f16) {
     const uint32_t a = d ^ 0x80808080u;
     const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    p0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) - bias);
-    p1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) - bias);
+    const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u));
+    const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u));
+    p0 = __builtin_bit_cast(uint32_t, lo - bias);
+    p1 = __builtin_bit_cast(uint32_t, hi - bias);
 }
 __device__ __forceinline__ void widen4(uint32_t d, uint32_t& p0, uint32_t& p1, bf16) {
     const float f0 = (float)(int8_t)(d & 0xff), f1 = (float)(int8_t)((d >> 8) & 0xff);
@@ -986,9 +988,9 @@ static int dot4_chunks(int K) {
 }
 
 // Grid for M >= 3: at most DOT4_BLOCKS_PER_CU workgroups per CU that are resident together (fewer when the registers
-// of a long K allow fewer), the same number on every CU, rows grid-strided over their wavefronts.  At K = 5120, N = 17408 with
-// non-temporal weight loads: M=1 16.9 -> 15.1 us, M=2 19.3 -> 15.8 us against one wavefront per two rows with
-// ordinary loads (the non-temporal loads alone: 15.1 and 17.6 us).
+// of a long K allow fewer), the same number on every CU, rows grid-strided over their wavefronts.  At K = 5120,
+// N = 17408 with non-temporal weight loads: M=1 16.9 -> 15.1 us, M=2 19.3 -> 15.8 us against one wavefront per two
+// rows with ordinary loads (the non-temporal loads alone: 15.1 and 17.6 us).
 constexpr int DOT4_BLOCKS_PER_CU = 4;
 // M <= 2 instead: one wavefront per workgroup and ceil(N / DOT4_ROWS_PER_WAVE) of them, so that every wavefront has
 // the same number of rows (four workgroups of four wavefronts per CU leave 4.25 rows per wavefront at N = 17408, a
@@ -1195,7 +1197,8 @@ static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
         &gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD>);
     static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
     (void)attr;
-    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
+    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD>
+        <<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
         p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
 }
 
@@ -1241,7 +1244,8 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
         }
         return;
     }
-    constexpr int SUB = GemmCfg<SmallCfg::WM, SmallCfg::WN, SmallCfg::FM, SmallCfg::FN, SmallCfg::KB, SmallCfg::NS>::SUB;
+    constexpr int SUB =
+        GemmCfg<SmallCfg::WM, SmallCfg::WN, SmallCfg::FM, SmallCfg::FN, SmallCfg::KB, SmallCfg::NS>::SUB;
     if (policy == 2) {
         launch_gemm_cfg<T, EPI, SmallCfg>(p, 0, tiles * SUB);
         return;
