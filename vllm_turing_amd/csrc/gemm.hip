@@ -29,9 +29,9 @@
 //    conflict-free, and the operand fragments of the next 32-byte sub-step read from LDS during the current one's
 //    MFMAs; workgroups remapped so the tiles resident on one XCD share A rows and W rows in that XCD's L2.  Where the
 //    tiles leave a last partial round over the CUs, that round runs as 128 x 128 quarter tiles (4 wavefronts of
-//    64 x 64, two workgroups per CU), or 64 x 128 eighth tiles where the quarters would leave half the CUs idle, so
-//    it spreads over the whole chip.  33..128 rows (and 129..256 against small N) run on 64 x 128 or 64 x 64 tiles
-//    with 4 K stages in flight.  The next stage's loads go out in slices between the MFMA blocks of the first
+//    64 x 64: two workgroups per CU, or one with 4 K stages in flight where they fit in one round), so it spreads
+//    over the whole chip.  33..128 rows (and 129..256 against small N) run on 64 x 128 or 64 x 64 tiles with 4 K
+//    stages in flight.  The next stage's loads go out in slices between the MFMA blocks of the first
 //    sub-steps.  The epilogue goes through LDS so that every global store writes whole lines, non-temporally.
 //    Large-M epilogue (csrc/w8a8_big.cu:26-35).
 //
@@ -1155,10 +1155,13 @@ struct SmallCfg {
     static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128, NS = 2, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
-// Tiny configuration: 64 x 128 eighth tiles, 2 x 2 wavefronts of 32 x 64 (48 KB: three workgroups per CU), for a last
-// round of so few super tiles that the quarter tiles would put two workgroups on some CUs and one on others.
-struct TinyCfg {
-    static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 2, SPLIT = 0;
+// The quarter tiles with 4 K stages in LDS (128 KB, one workgroup per CU), for a remainder whose quarter tiles fit in
+// one round at one per CU: each workgroup keeps three stages of its rows in flight, which a few workgroups streaming
+// long K from HBM need.  Weights rotated beyond the MALL: N = 5120, K = 17408, M = 512 122.3 -> 86.0 us; N = 5120,
+// K = 5120, M = 512 43.1 -> 30.6 us; M = 512, N = 34816 (16 remaining super tiles) 126.5 -> 120.7 us against 64 x 128
+// eighth tiles with 2 stages, which it replaces; 3 stages measured within 2% of 4.
+struct SmallDeepCfg {
+    static constexpr int WM = 2, WN = 2, FM = 2, FN = 2, KB = 128, NS = 4, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
 // Mid configurations for 33..128 rows, where a tile row holds all of M: 64-row tiles with 4 K stages in LDS, so that
@@ -1260,11 +1263,9 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
     }
     if (full > 0 && longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, full);
     else if (full > 0) launch_gemm_cfg<T, EPI, MainCfg>(p, 0, full);
-    // the remainder as quarter tiles, or as eighth tiles where the quarters would leave at least half the CUs idle:
-    // M = 512, N = 34816 (16 remaining super tiles) 106.2 -> 100.2 us; where the quarters already cover the CUs the
-    // eighth tiles' extra fragment reads cost more than their balance gains (M = 512, N = 12288: 40.4 -> 45.7 us)
-    constexpr int SUBT = GemmCfg<TinyCfg::WM, TinyCfg::WN, TinyCfg::FM, TinyCfg::FN, TinyCfg::KB, TinyCfg::NS>::SUB;
-    if (2 * rem * SUB <= cus) launch_gemm_cfg<T, EPI, TinyCfg>(p, full, rem * SUBT);
+    // the remainder as quarter tiles: with 4 K stages where they fit in one round at one workgroup per CU, else with 2
+    // (two workgroups per CU)
+    if (rem * SUB <= cus) launch_gemm_cfg<T, EPI, SmallDeepCfg>(p, full, rem * SUB);
     else launch_gemm_cfg<T, EPI, SmallCfg>(p, full, rem * SUB);
 }
 
