@@ -432,7 +432,8 @@ def bench_headline(torch, L, st, dev, args):
     print(f"[bench] GEMM M={Mg} K={Kg} N={Ng}", file=sys.stderr, flush=True)
     # 2 s of back-to-back GEMMs first, untimed: the clock sample, and the warm-up that lets the clock settle (the
     # first ~100 launches after the memory-bound sections run ~7% slower than the sustained rate)
-    sclk = sclk_under_load(torch, lambda: gemm(0))
+    rot = iter(range(1 << 30))
+    sclk = sclk_under_load(torch, lambda: gemm(next(rot)))   # the same rotation as the timed launches
     print(f"[bench] gfx clock under GEMM load: {sclk} MHz", file=sys.stderr, flush=True)
     gemm_steps = max(20, args.steps // 20)
     ms_gemm, n_gemm = graph_time(torch, gemm, gcopies, gemm_steps, max(4, args.warmup // 20))
