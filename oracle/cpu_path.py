@@ -1,4 +1,5 @@
-"""The reference's W8A8 linear restated as a vectorised CPU path: TEST AND CPU-BASELINE INFRASTRUCTURE ONLY.
+"""The reference's W8A8 linear restated as a vectorised CPU path: test infrastructure and the CPU baseline leg of
+bench.py only.
 
 This is what bench.py times as the CPU baseline (kind "port") and what the tests use to check full-size shapes
 cheaply: torch's CPU int8 matmul (torch._int_mm, exact int32 results) plus the same float32 epilogue chains as

@@ -654,7 +654,7 @@ def test_prefill_config_sampled(L, M):
 
 def test_mlp_tail_fused(L):
     """tailoverlap.py:145-151's fused tail: residual add + RMSNorm + quant -> gate_up -> SiLU*up+quant -> down, every
-    intermediate bit-exact (M = 64, the C4 widths, GemmaRMSNorm weight 1 + w)."""
+    intermediate bit-exact (M = 64, hidden 5120, intermediate 17408, GemmaRMSNorm weight 1 + w)."""
     say("mlp tail fused")
     from vllm_turing_amd import workloads, mlp_tail
     from vllm_turing_amd.normquant import gemma_weight
@@ -705,7 +705,8 @@ def test_checkpoint_layers_forward(L, tmp_path):
 
 
 def test_mlp_chain_small(L):
-    """gate_up GEMM -> silu_mul_quant -> down GEMM, every intermediate bit-exact (M = 64, the C4 widths)."""
+    """gate_up GEMM -> silu_mul_quant -> down GEMM, every intermediate bit-exact (M = 64, hidden 5120,
+    intermediate 17408)."""
     say("mlp chain")
     from vllm_turing_amd import workloads, per_token_quant, mlp_quantized
     from vllm_turing_amd.tailoverlap import silu_mul_quant
