@@ -18,7 +18,7 @@
 //    up to 16 activation rows per MFMA as the B operand.  The K slices of a tile meet in LDS.  The launch picks the
 //    wavefronts, ring depth and tiles per workgroup from how the tiles fill the resident slots.  Small-M epilogue
 //    chain (the large-M one when it serves the prefill entry).
-//  * w8a16_dot_kernel (the int8 LM head: fp16 / bf16 activations, M <= 3): the dot4 kernel's weight stream, each
+//  * w8a16_dot_kernel (the int8 LM head: fp16 / bf16 activations, M <= 2): the dot4 kernel's weight stream, each
 //    weight widened exactly to 16-bit pairs for v_dot2_f32_{f16,bf16}; float32 sums.
 //  * w8a16_kernel (the int8 LM head, the rest of M <= 32): the LDS-ring weight stream (two or three 16-row tiles per
 //    workgroup sharing each activation fragment) with each int8 fragment widened to fp16 / bf16 in registers for
@@ -838,7 +838,7 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
         }
 }
 
-// w8a16_dot_kernel: M <= 3 rows of the int8 LM head through the VALU.  The weight stream of gemv_dot4_kernel (each
+// w8a16_dot_kernel: M <= 2 rows of the int8 LM head through the VALU.  The weight stream of gemv_dot4_kernel (each
 // wavefront instruction reads 1 KB of one weight row, non-temporally; lane l owns the 16-byte chunks l, l + 64, ...;
 // rows grid-strided over at most four resident workgroups per CU, the next row's loads issued before this row's math);
 // each lane widens its 16 weights to 16-bit pairs (fp16 by the exact bit trick, bf16 through float32) and
@@ -1375,8 +1375,9 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
 // ---------------------------------------------------------------------------------------------------------------------
 // W8A16 (int8 LM head)
 // ---------------------------------------------------------------------------------------------------------------------
-// M = 1 up to K = 8192 and M = 2, 3 up to K = 5120 (the activations' registers) take the VALU kernel (M = 3 at
-// N = 248320: 289 -> 229 us; four rows take 256 registers, one wavefront per SIMD, and lose: 298 -> 387 us).
+// M = 1 up to K = 8192 and M = 2 up to K = 5120 (the activations' registers) take the VALU kernel.  Three rows take
+// fewer wavefronts per SIMD and tie with the MFMA kernel in bf16 (N = 248320, K = 5120: 219.5 against 218.3 us) and
+// lose in fp16 (227.8 against 216.4 us); four rows take 256 registers, one wavefront per SIMD, and lose by more.
 constexpr int W8A16_DOT_MAX_CH_M1 = 8, W8A16_DOT_MAX_CH_M2 = 5;
 
 template <typename T, int M, int CH, bool GATHER>
@@ -1409,8 +1410,6 @@ static bool launch_w8a16_dot(const void* x, const void* w, const void* s, const 
                             : launch_w8a16_dot_m<T, 1, false>(x, w, s, bias, out, N, K, w_rows, rows, st);
     if (M == 2) return rows ? launch_w8a16_dot_m<T, 2, true>(x, w, s, bias, out, N, K, w_rows, rows, st)
                             : launch_w8a16_dot_m<T, 2, false>(x, w, s, bias, out, N, K, w_rows, rows, st);
-    if (M == 3) return rows ? launch_w8a16_dot_m<T, 3, true>(x, w, s, bias, out, N, K, w_rows, rows, st)
-                            : launch_w8a16_dot_m<T, 3, false>(x, w, s, bias, out, N, K, w_rows, rows, st);
     return false;
 }
 
