@@ -66,10 +66,13 @@ def traffic_from_profiles(key):
 
 
 def graph_time(torch, launch, n_launch_per_graph, steps, warmup, min_warm_s=0.05):
-    """Capture n launches in a HIP graph, replay; return ms per launch over `steps` launches.  The untimed warm-up
-    replays are at least `warmup` launches and at least `min_warm_s` seconds of GPU work, just before the timed
-    replays (a synchronization between them): after an idle gap (the capture) a GEMM's launches were measured slowing from 224 to 266 us and
-    settling at 218 us only after ~100 launches (the power management's transient), which a short warm-up would time."""
+    """Capture n launches in a HIP graph, replay; return ms per launch over `steps` launches (rounded up to whole
+    replays) and the number of launches timed.  The untimed warm-up replays are at least `warmup` launches and at
+    least `min_warm_s` seconds of GPU work (after an idle gap such as the capture a GEMM's launches were measured
+    slowing from 224 to 266 us and settling at 218 us only after ~100 launches, the power management's transient).
+    The timed replays are queued right behind the warm-up ones with no host synchronization between them, so the
+    timed region starts on a busy GPU instead of paying the restart after an idle gap (a host synchronization there
+    added ~1.5 us per launch to a 20-launch timed region of 14.3 us GEMVs)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -92,7 +95,6 @@ def graph_time(torch, launch, n_launch_per_graph, steps, warmup, min_warm_s=0.05
     reps = max(1, (steps + n_launch_per_graph - 1) // n_launch_per_graph)
     for _ in range(reps_w):
         g.replay()
-    torch.cuda.synchronize()
     e0.record()
     for _ in range(reps):
         g.replay()
@@ -145,6 +147,21 @@ def sclk_under_load(torch, launch, seconds=2.0):
         return None
     clocks.sort()
     return clocks[len(clocks) // 2]
+
+
+def host_cpu():
+    """(os.cpu_count(), the CPU model name lscpu reports or None) of this host."""
+    import subprocess
+    model = None
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20)
+        for line in r.stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return os.cpu_count(), model
 
 
 def cpu_time(fn, budget_s):
@@ -228,8 +245,15 @@ def bench_mlp(torch, L, st, dev):
     x = c["x"].to(dev)
     res = (torch.randn(M, H, generator=g) * 0.5).to(torch.bfloat16).to(dev)
     nw = (1.0 + torch.randn(H, generator=g) * 0.1).to(torch.bfloat16).to(dev)
-    wgu, swgu = c["w_gate_up"].to(dev), c["sw_gate_up"].to(dev)
-    wd, swd = c["w_down"].to(dev), c["sw_down"].to(dev)
+    # three copies of each weight, rotated per launch (gate_up 3 x 178 MB, down 3 x 89 MB): every launch reads its
+    # weights from HBM, as a layer stack does, instead of from the 256 MB MALL
+    copies = 3
+    gw = torch.Generator(device=dev).manual_seed(31)
+    wgus = [c["w_gate_up"].to(dev)] + [torch.randint(-127, 128, (2 * I, H), dtype=torch.int8, device=dev, generator=gw)
+                                       for _ in range(copies - 1)]
+    wds = [c["w_down"].to(dev)] + [torch.randint(-127, 128, (H, I), dtype=torch.int8, device=dev, generator=gw)
+                                   for _ in range(copies - 1)]
+    swgu, swd = c["sw_gate_up"].to(dev), c["sw_down"].to(dev)
     x_q = torch.empty(M, H, dtype=torch.int8, device=dev)
     x_s = torch.empty(M, dtype=torch.float32, device=dev)
     gu = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=dev)
@@ -244,21 +268,22 @@ def bench_mlp(torch, L, st, dev):
             raise RuntimeError("rms_norm_quant")
 
     def gate_up(i=0):
-        linear_launch(L, st, x_q, x_s, wgu, swgu, gu, M, 2 * I, H, 1)
+        linear_launch(L, st, x_q, x_s, wgus[i % copies], swgu, gu, M, 2 * I, H, 1)
 
     def silu(i=0):
         if L.silu_mul_quant_bf16(gu.data_ptr(), a_q.data_ptr(), a_s.data_ptr(), M, I, st()) != 0:
             raise RuntimeError("silu_mul_quant_bf16")
 
     def down(i=0):
-        linear_launch(L, st, a_q, a_s, wd, swd, out, M, H, I, 1)
+        linear_launch(L, st, a_q, a_s, wds[i % copies], swd, out, M, H, I, 1)
 
     def chain(i=0):
-        norm_quant(); gate_up(); silu(); down()
+        norm_quant(i); gate_up(i); silu(i); down(i)
 
     res_d = {"workload": f"MLP tail M={M} as tailoverlap.py:145-151 runs it: residual add + RMSNorm + int8 quant "
                          f"[{M},{H}] -> gate_up N={2 * I} K={H} -> SiLU*up+quant I={I} -> down N={H} K={I}, bf16, "
-                         f"SmoothQuant-scaled N(0,1) activations with 0.5% outliers"}
+                         f"SmoothQuant-scaled N(0,1) activations with 0.5% outliers, {copies} weight copies "
+                         f"rotated per launch ({copies * 3 * I * H / 1e6:.0f} MB > 256 MB MALL)"}
     # about 1 s of untimed chains first: the clock settles under the GEMMs' load (their first ~20 ms after
     # memory-bound work run ~7% slower)
     t_end = time.time() + 1.0
@@ -266,8 +291,8 @@ def bench_mlp(torch, L, st, dev):
         chain()
         torch.cuda.synchronize()
     t = {}
-    for name, fn, n in (("norm_quant", norm_quant, 10), ("gate_up", gate_up, 4), ("silu_mul_quant", silu, 4),
-                        ("down", down, 4), ("chain", chain, 2)):
+    for name, fn, n in (("norm_quant", norm_quant, 10), ("gate_up", gate_up, 3), ("silu_mul_quant", silu, 4),
+                        ("down", down, 3), ("chain", chain, 3)):
         ms, _ = graph_time(torch, fn, n, 4 * n, n)
         t[name] = ms
     ops_gu, ops_d = 2.0 * M * 2 * I * H, 2.0 * M * H * I
@@ -381,6 +406,22 @@ def bench_headline(torch, L, st, dev, args):
     gemv_gbs = gemv_bytes / (ms_gemv * 1e-3) / 1e9
     print(f"[bench] GEMV {ms_gemv * 1e3:.2f} us/launch, {gemv_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
+    # the achievable ceiling: a read-only stream of the same rotated weight copies through the GEMV's load path
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def read(i):
+        rc = L.hbm_read(ws[i % copies].data_ptr(), N * K, sink.data_ptr(), st())
+        if rc != 0:
+            raise RuntimeError(f"hbm_read {rc}")
+
+    ms_read, _ = graph_time(torch, read, 4 * copies, args.steps, args.warmup)
+    read_gbs = N * K / (ms_read * 1e-3) / 1e9
+    read_ceiling = {"workload": f"read-only stream of the same {copies} rotated {N * K / 1e6:.0f} MB weight copies "
+                                f"(16-byte non-temporal loads, the GEMV's load path, no math)",
+                    "us": round(ms_read * 1e3, 2), "gbs": round(read_gbs, 1),
+                    "frac": round(read_gbs / HBM_PEAK_GBS, 4), "gemv_over_read": round(gemv_gbs / read_gbs, 4)}
+    print(f"[bench] read ceiling {ms_read * 1e3:.2f} us/launch, {read_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
     # the other decode batch sizes of the same projection (M = 2, 4, 8), same weights and method
     decode_m = {}
     for Md in (2, 4, 8, 16, 32, 64):
@@ -440,6 +481,22 @@ def bench_headline(torch, L, st, dev, args):
     gemm_ops = 2.0 * Mg * Ng * Kg
     gemm_tops = gemm_ops / (ms_gemm * 1e-3) / 1e12
     print(f"[bench] GEMM {ms_gemm * 1e3:.1f} us/launch, {gemm_tops:.0f} TOPS", file=sys.stderr, flush=True)
+    # the other prefill chunk sizes of the same projection, same rotated weights: the first Mo rows of the activations
+    gemm_other = {}
+    for Mo in (512, 2048):
+        outo = torch.empty(Mo, Ng, dtype=torch.bfloat16, device=dev)
+
+        def gemm_o(i, Mo=Mo, outo=outo):
+            rc = L.w8a8_scaled_mm(a_q.data_ptr(), wgs[i % gcopies].data_ptr(), a_s.data_ptr(), swg.data_ptr(),
+                                  bias.data_ptr(), outo.data_ptr(), Mo, Ng, Kg, 1, 1, 1, st())
+            if rc != 0:
+                raise RuntimeError(f"w8a8_scaled_mm M={Mo}: {rc}")
+
+        ms_o, _ = graph_time(torch, gemm_o, 2 * gcopies, 8 * gcopies, 2 * gcopies)
+        tops_o = 2.0 * Mo * Ng * Kg / (ms_o * 1e-3) / 1e12
+        gemm_other[f"M{Mo}"] = {"us": round(ms_o * 1e3, 2), "tops": round(tops_o, 1),
+                                "frac": round(tops_o / INT8_PEAK_TOPS, 4)}
+    print(f"[bench] GEMM M=512 / 2048: {gemm_other}", file=sys.stderr, flush=True)
     del wgs
 
     # ---- quant kernels ------------------------------------------------------------------------------------------------
@@ -520,17 +577,20 @@ def bench_headline(torch, L, st, dev, args):
     if not args.no_cpu:
         from oracle import cpu_path
         threads = torch.get_num_threads()
+        n_cpus, cpu_model = host_cpu()
         xc, wc, swc = c["x"], c["w"], c["sw"]
         t_gemv, n_cpu = cpu_time(lambda: cpu_path.linear(xc, wc, swc, None, torch.float16), 10.0)
         cpu = {"value": round(gemv_bytes / t_gemv / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"M=1 K={K} N={N} quant+int_mm+dequant, {n_cpu} calls, median"}
+               "sample": f"M=1 K={K} N={N} quant+int_mm+dequant, {n_cpu} calls, median",
+               "host_cpus": n_cpus, "cpu_model": cpu_model}
         Ms = 256
         xs_ = p["x"][:Ms]
         t_g, n_g = cpu_time(lambda: cpu_path.linear(xs_, p["w"], p["sw"], p["bias"], torch.bfloat16), 10.0)
         cpu_gemm = {"value": round(2.0 * Ms * Ng * Kg / t_g / 1e12, 3), "unit": "TOPS", "cores": threads,
-                    "kind": "port", "sample": f"M={Ms} of 4096 rows, K={Kg} N={Ng}, {n_g} calls, median"}
-        print(f"[bench] CPU GEMV {cpu['value']} GB/s, GEMM {cpu_gemm['value']} TOPS on {threads} threads",
-              file=sys.stderr, flush=True)
+                    "kind": "port", "sample": f"M={Ms} of 4096 rows, K={Kg} N={Ng}, {n_g} calls, median",
+                    "host_cpus": n_cpus, "cpu_model": cpu_model}
+        print(f"[bench] CPU GEMV {cpu['value']} GB/s, GEMM {cpu_gemm['value']} TOPS on {threads} threads "
+              f"(host: {n_cpus} CPUs, {cpu_model})", file=sys.stderr, flush=True)
 
     result = {
         "metric": METRIC,
@@ -551,6 +611,7 @@ def bench_headline(torch, L, st, dev, args):
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("gemv_m1")},
         "cpu_baseline": cpu,
+        "gemv_read_ceiling": read_ceiling,
         "decode_other_m": {"workload": f"decode W8A8 K={K} N={N}, fp16 out, same rotated weights, the entry the reference "
                                        f"dispatches at each M (w8a8_gemv <= 12, w8a8_mma <= 32, w8a8_big above)",
                            **decode_m},
@@ -560,6 +621,8 @@ def bench_headline(torch, L, st, dev, args):
                  "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS,
                               "unit": "TOPS", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
                               "traffic": traffic_from_profiles("gemm_m4096")},
+                 "other_m": {"workload": f"the same projection (K={Kg}, N={Ng}, bias, bf16, rotated weights) at "
+                                         f"the other prefill chunk sizes", **gemm_other},
                  "sclk_mhz": sclk,
                  "frac_at_sclk": (round(gemm_tops / (INT8_PEAK_TOPS * sclk / SCLK_MAX_MHZ), 4) if sclk else None),
                  "cpu_baseline": cpu_gemm},

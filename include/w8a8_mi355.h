@@ -86,10 +86,25 @@ int ar8_dequant_sum_ranks(const void* gathered, void* out, int n, int ranks, voi
 int w8a16_gemv(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K, int dtype,
                void* stream);
 
-/* The same over the gathered weight rows rows[0..N) (int32, indexes into the w_rows rows of w; out is compact), as
- * csrc/w8a16_gemv.cu:145-146 for a pruned draft vocabulary; w_rows bounds the reads and has no counterpart there. */
+/* The same over the gathered weight rows rows[0..N) (int32 indexes into w; out is compact), for a pruned draft
+ * vocabulary; rows = NULL computes all N rows.  Replaces vllm_turing/csrc/w8a16_gemv.cu:145-146 (same 11 arguments,
+ * bound by vllm_turing/draftvocab.py:269 and tests/test_dhead.py:83).  As there, every index must name a row of w. */
 int w8a16_gemv_rows(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
-                    int dtype, const void* rows, int w_rows, void* stream);
+                    int dtype, const void* rows, void* stream);
+
+/* The gathered form with w's row count w_rows: indices are clamped to [0, w_rows) so the loads stay inside w.  No
+ * counterpart in the reference (its indices are trusted).  Returns -1 on bad arguments or a null rows. */
+int w8a16_gemv_rows_bounded(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
+                            int K, int dtype, const void* rows, int w_rows, void* stream);
+
+/* The int8 LM head for 5..64 rows with fp16 activations, the reference's tensor-core entry (vllm_turing/csrc/
+ * w8a16_mma.cu:176-191, same arguments, bound by vllm_turing/lmhead.py:33-37,77): out [M, N] fp16 = x [M, K] fp16
+ * times w [N, K] int8 with scales s [N] and bias [N] fp16 or NULL, float32 sums.  Returns -1 for M outside 1..64, an
+ * odd N, or K not a multiple of cfg's k-tile (cfg 0: 128, 1: 256, other: 512 bytes); -2 for the 512-byte k-tile with
+ * M > 32 (the reference's shared-memory limit); -1 on null or misaligned x / w; else the launch error.  Every cfg runs
+ * the same kernel, so outputs do not depend on cfg. */
+int w8a16_mma(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K, int cfg,
+              void* stream);
 
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
  * checks: kernel 0 the small-M MFMA streaming kernel (M <= 64), 1 the prefill kernel as dispatched, 2 the v_dot4
@@ -113,6 +128,13 @@ int silu_table(void* out, int dtype, void* stream);
  * or bf16 (dtype 1), the rounding every 16-bit output of this library goes through.  No counterpart in the
  * reference.  Returns -1 on bad arguments, else the HIP launch error. */
 int f32_to_16(const void* x, void* out, long n, int dtype, void* stream);
+
+/* Test export: a read-only stream of `bytes` bytes of src (16-byte aligned, bytes % 16 == 0) through the weight-
+ * streaming GEMV's load path (16-byte non-temporal loads, 1 KB per wavefront instruction), the data discarded: the
+ * achievable read rate the GEMV is measured against.  sink: one int of device memory, written only if the XOR of all
+ * words read equals 0x5a3c96e1.  No counterpart in the reference.  Returns -1 on bad arguments, else the launch
+ * error. */
+int hbm_read(const void* src, long bytes, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -78,7 +78,26 @@ def test_argument_validation_codes(L):
     assert L.w8a16_gemv(16, 16, 16, None, 16, 33, 64, 64, 0, None) == -1        # M <= 32
     assert L.w8a16_gemv(16, 16, 16, None, 16, 4, 64, 72, 0, None) == -1         # K % 16
     assert L.w8a16_gemv(16, 16, 16, None, 16, 4, 64, 64, 2, None) == -1         # dtype
-    assert L.w8a16_gemv_rows(16, 16, 16, None, 16, 4, 64, 64, 0, None, 64, None) == -1   # rows required
+    # the reference's 11-argument gathered entry (csrc/w8a16_gemv.cu:145-147): rows = NULL means all rows
+    assert L.w8a16_gemv_rows(16, 16, 16, None, 16, 33, 64, 64, 0, None, None) == -1     # M <= 32
+    assert L.w8a16_gemv_rows(16, 16, 16, None, 16, 4, 64, 72, 0, 16, None) == -1       # K % 16
+    assert L.w8a16_gemv_rows_bounded(16, 16, 16, None, 16, 4, 64, 64, 0, None, 64, None) == -1   # rows required
+    assert L.w8a16_gemv_rows_bounded(16, 16, 16, None, 16, 4, 64, 64, 0, 16, 0, None) == -1      # w_rows >= 1
+    # w8a16_mma (csrc/w8a16_mma.cu:176-191): -1 for M outside 1..64, odd N, K not a multiple of cfg's k-tile;
+    # -2 for the 512-byte k-tile above 32 rows
+    assert L.w8a16_mma(16, 16, 16, None, 16, 0, 64, 512, 2, None) == -1
+    assert L.w8a16_mma(16, 16, 16, None, 16, 65, 64, 512, 1, None) == -1
+    assert L.w8a16_mma(16, 16, 16, None, 16, 8, 63, 512, 2, None) == -1
+    assert L.w8a16_mma(16, 16, 16, None, 16, 8, 64, 384, 2, None) == -1            # 512-byte k-tile
+    assert L.w8a16_mma(16, 16, 16, None, 16, 8, 64, 320, 1, None) == -1            # 256-byte k-tile
+    assert L.w8a16_mma(16, 16, 16, None, 16, 8, 64, 192, 0, None) == -1            # 128-byte k-tile
+    assert L.w8a16_mma(16, 16, 16, None, 16, 33, 64, 5120, 2, None) == -2
+    assert L.w8a16_mma(8, 16, 16, None, 16, 8, 64, 512, 2, None) == -1             # x 16-byte aligned
+    assert L.w8a16_mma(None, 16, 16, None, 16, 8, 64, 512, 2, None) == -1
+    assert L.hbm_read(None, 1024, 16, None) == -1
+    assert L.hbm_read(16, 1000, 16, None) == -1                                    # bytes % 16
+    assert L.hbm_read(8, 1024, 16, None) == -1                                     # 16-byte aligned
+    assert L.silu_table(16, 4, None) == -1                                         # 0..3
     assert L.ar8_quant(16, 16, 100, None) == -1                                 # n % 128
     assert L.ar8_quant(8, 16, 128, None) == -1                                  # x 16-byte aligned
     assert L.ar8_quant(16, 16, 0, None) == 0

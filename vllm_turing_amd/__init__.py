@@ -19,7 +19,7 @@ import os
 logger = logging.getLogger("vllm.turing_amd")
 _registered = False
 
-from . import ar8, lmhead, normquant, quantfuse, w8a8  # noqa: E402,F401  (defines the custom ops)
+from . import ar8, hooks, lmhead, normquant, quantfuse, w8a8  # noqa: E402,F401  (defines the custom ops)
 from .linear import W8A8Linear, W8A8LinearMethod  # noqa: E402,F401
 from .normquant import rms_norm_dynamic_per_token_quant  # noqa: E402,F401
 from .quantfuse import per_token_quant, quant_torch, scaled_int8_quant  # noqa: E402,F401
@@ -28,15 +28,16 @@ from .w8a8 import cutlass_scaled_mm  # noqa: E402,F401
 
 
 def register():
-    """Install the hooks into vllm._custom_ops (quantfuse before w8a8, as vllm_turing/__init__.py:61-65)."""
+    """The vLLM plugin entry point (vllm_turing/__init__.py:38-72): install the hooks in the reference's order (the
+    fused norm + quant producer in tailoverlap's slot, then quantfuse, w8a8, lmhead), once per process; nothing when
+    VLLM_TURING_DISABLE=1.  Returns {hook: installed} for this call ({} when disabled or already registered)."""
     global _registered
     if _registered or os.environ.get("VLLM_TURING_DISABLE", "0") == "1":
-        return
+        return {}
     _registered = True
-    q = quantfuse.install()
-    n = normquant.install()
-    m = w8a8.install()
-    lmhead.install()
-    logger.info("vllm_turing_amd: scaled_int8_quant hook %s, rms_norm_dynamic_per_token_quant hook %s, "
-                "cutlass_scaled_mm hook %s (GEMV up to M=%d)", "on" if q else "off", "on" if n else "off",
-                "on" if m else "off", w8a8.MAX_M)
+    done = {}
+    for name, mod in (("normquant", normquant), ("quantfuse", quantfuse), ("w8a8", w8a8), ("lmhead", lmhead)):
+        done[name] = bool(mod.install())
+    logger.info("vllm_turing_amd hooks: %s (GEMV up to M=%d)",
+                ", ".join(f"{k} {'on' if v else 'off'}" for k, v in done.items()), w8a8.MAX_M)
+    return done

@@ -6,6 +6,9 @@ to a temporary name and renamed into place (:53), and the loaded handle is cache
 file is compiled to an object in parallel, then linked.  There is no CPU fallback: if the library cannot be built or
 loaded, load() raises.
 
+Before compiling, the SiLU lookup tables are generated into build/silu_table.inc (silu_table.py), which quant.hip
+includes as read-only device data.
+
 Flags: -O3, -ffp-contract=off (every multiply-add fusion in the kernels is an explicit __builtin_fmaf, so the float
 epilogues round exactly where the reference rounds), correctly rounded float32 division (hipcc's default, never
 -ffast-math), and the packed-FP32 instructions switched off.
@@ -41,9 +44,13 @@ def _sources():
     return sorted(glob.glob(os.path.join(_CSRC, "*.hip")))
 
 
+_GENERATOR = os.path.join(_HERE, "silu_table.py")
+_SILU_INC = os.path.join(_BUILD, "silu_table.inc")
+
+
 def _deps():
     return _sources() + sorted(glob.glob(os.path.join(_CSRC, "*.h"))) + \
-        sorted(glob.glob(os.path.join(_INCLUDE, "*.h")))
+        sorted(glob.glob(os.path.join(_INCLUDE, "*.h"))) + [_GENERATOR]
 
 
 def _hipcc():
@@ -70,11 +77,13 @@ def build(name=LIB_NAME, force=False, verbose=False):
         if not force and not stale(name):
             return so
         hipcc = _hipcc()
+        from . import silu_table
+        silu_table.write_include(_SILU_INC)
         objs = []
 
         def compile_one(src):
             obj = os.path.join(_BUILD, os.path.basename(src)[:-4] + ".o")
-            cmd = [hipcc, *HIPCC_FLAGS, f"-I{_INCLUDE}", "-c", src, "-o", obj + ".tmp"]
+            cmd = [hipcc, *HIPCC_FLAGS, f"-I{_INCLUDE}", f"-I{_BUILD}", "-c", src, "-o", obj + ".tmp"]
             r = subprocess.run(cmd, capture_output=True, text=True)
             if r.returncode != 0:
                 raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

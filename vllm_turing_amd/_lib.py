@@ -18,7 +18,9 @@ SIGNATURES = {
     "silu_mul_quant": [_vp] * 3 + [_i] * 2 + [_vp],
     "silu_mul_quant_bf16": [_vp] * 3 + [_i] * 2 + [_vp],
     "w8a16_gemv": [_vp] * 5 + [_i] * 4 + [_vp],
-    "w8a16_gemv_rows": [_vp] * 5 + [_i] * 4 + [_vp, _i, _vp],
+    "w8a16_gemv_rows": [_vp] * 5 + [_i] * 4 + [_vp, _vp],
+    "w8a16_gemv_rows_bounded": [_vp] * 5 + [_i] * 4 + [_vp, _i, _vp],
+    "w8a16_mma": [_vp] * 5 + [_i] * 4 + [_vp],
     "ar8_quant": [_vp, _vp, _i, _vp],
     "ar8_dequant_sum": [_vp, _vp, _i, _vp],
     "ar8_dequant_sum_ranks": [_vp, _vp, _i, _i, _vp],
@@ -27,6 +29,7 @@ SIGNATURES = {
     "silu_table": [_vp, _i, _vp],
     "silu_mul_quant_path": [_vp] * 3 + [_i] * 4 + [_vp],
     "f32_to_16": [_vp, _vp, _l, _i, _vp],
+    "hbm_read": [_vp, _l, _vp, _vp],
 }
 
 _lib = None

@@ -1373,6 +1373,33 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// hbm_read: a read-only stream of a buffer (the ceiling the weight-streaming GEMV is measured against)
+// ---------------------------------------------------------------------------------------------------------------------
+// The GEMV's loads without its math: 16 bytes per lane, non-temporal, each wavefront instruction 1 KB contiguous, four
+// in flight per lane, grid-strided over HBM_READ_BLOCKS_PER_CU workgroups of 256 per CU.  The words read are XORed
+// together and the result is stored only if it equals a value no real input produces in practice, so the kernel
+// writes nothing while the loads cannot be removed.
+constexpr int HBM_READ_BLOCKS_PER_CU = 8, HBM_READ_UNROLL = 4;
+
+__global__ void __launch_bounds__(256) hbm_read_kernel(const v4i* __restrict__ src, long n16, int* __restrict__ sink) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    int x = 0;
+    for (; i + (HBM_READ_UNROLL - 1) * stride < n16; i += HBM_READ_UNROLL * stride) {
+        v4i v[HBM_READ_UNROLL];
+#pragma unroll
+        for (int u = 0; u < HBM_READ_UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < HBM_READ_UNROLL; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const v4i v = __builtin_nontemporal_load(src + i);
+        x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (x == 0x5a3c96e1) sink[0] = x;
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
 // W8A16 (int8 LM head)
 // ---------------------------------------------------------------------------------------------------------------------
 // M = 1 up to K = 8192 and M = 2 up to K = 5120 (the activations' registers) take the VALU kernel.  Three rows take
@@ -1462,11 +1489,57 @@ extern "C" int w8a16_gemv(const void* x, const void* w, const void* s, const voi
     return w8a16_entry(x, w, s, bias, out, M, N, K, dtype, N, nullptr, stream);
 }
 
-// The same over a gathered subset of weight rows (csrc/w8a16_gemv.cu:145-146,156-167): rows int32 [N] indexes the
-// w_rows rows of w; out [M, N] is compact over the subset.  w_rows (the row count of w, which bounds the loads) is an
-// argument the reference does not need.
+// The same over a gathered subset of weight rows, with the reference's arguments (csrc/w8a16_gemv.cu:145-146,156-167):
+// rows int32 [N] indexes rows of w and out [M, N] is compact over the subset; rows = null computes all N rows.  As
+// there, every index must name a row of w (the caller's guarantee, e.g. a draft vocabulary built from the head): the
+// library does not know w's row count, so indices are only clamped to the rows a 32-bit offset reaches
+// (2^31 / K); w8a16_gemv_rows_bounded takes that count and clamps to it.
 extern "C" int w8a16_gemv_rows(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N,
-                               int K, int dtype, const void* rows, int w_rows, void* stream) {
+                               int K, int dtype, const void* rows, void* stream) {
+    if (!rows) return w8a16_entry(x, w, s, bias, out, M, N, K, dtype, N, nullptr, stream);
+    if (K < 16) return -1;
+    const int reach = (int)(((1L << 31) - 1) / K);       // rows addressable by 32-bit buffer offsets
+    return w8a16_entry(x, w, s, bias, out, M, N, K, dtype, reach, static_cast<const int*>(rows), stream);
+}
+
+// The gathered form with the row count of w: indices are clamped to [0, w_rows), so a bad index reads a row of w
+// instead of memory past it.  No counterpart in the reference (whose rows are trusted).
+extern "C" int w8a16_gemv_rows_bounded(const void* x, const void* w, const void* s, const void* bias, void* out, int M,
+                                       int N, int K, int dtype, const void* rows, int w_rows, void* stream) {
     if (!rows) return -1;
     return w8a16_entry(x, w, s, bias, out, M, N, K, dtype, w_rows, static_cast<const int*>(rows), stream);
+}
+
+// The reference's tensor-core W8A16 entry (csrc/w8a16_mma.cu:176-191, same arguments and codes): x [M, K] fp16,
+// w [N, K] int8, s [N] float32, bias [N] fp16 or null, out [M, N] fp16; 1 <= M <= 64 and N even, else -1; cfg 0 / 1 /
+// other names the reference's k-tile of 128 / 256 / 512 bytes, and K must be a multiple of it (-1 otherwise); cfg
+// with 512-byte k-tiles refuses M > 32 with -2 as the reference's shared-memory limit does.  Every cfg runs the same
+// MFMA weight-streaming kernel here (in passes of at most 32 rows), so the outputs do not depend on cfg.  Also -1 on
+// null or misaligned pointers (x and w 16-byte aligned).  Returns the launch error otherwise.
+extern "C" int w8a16_mma(const void* x, const void* w, const void* s, const void* bias, void* out, int M, int N, int K,
+                         int cfg, void* stream) {
+    if (M < 1 || M > 64 || N % 2 != 0) return -1;
+    const int kt = cfg == 0 ? 128 : cfg == 1 ? 256 : 512;
+    if (K < kt || K % kt != 0) return -1;
+    if (kt == 512 && M > 32) return -2;
+    for (int r0 = 0; r0 < M; r0 += 32) {
+        const int rows = M - r0 < 32 ? M - r0 : 32;
+        const int rc = w8a16_entry(static_cast<const uint16_t*>(x) + (long)r0 * K, w, s, bias,
+                                   static_cast<uint16_t*>(out) + (long)r0 * N, rows, N, K, DT_F16, N, nullptr, stream);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+// Test export: stream `bytes` bytes of src (16-byte aligned, bytes % 16 == 0) through the GEMV's load path and discard
+// them (sink: one int, written only in the improbable case described at hbm_read_kernel).  No counterpart in the
+// reference.  Returns -1 on bad arguments, else the launch error.
+extern "C" int hbm_read(const void* src, long bytes, void* sink, void* stream) {
+    if (!src || !sink || bytes < 16 || bytes % 16 != 0 || (uintptr_t)src % 16 != 0) return -1;
+    const long n16 = bytes / 16;
+    const long need = (n16 + 255) / 256;
+    const long cap = (long)cu_count() * HBM_READ_BLOCKS_PER_CU;
+    hbm_read_kernel<<<(int)(need < cap ? need : cap), 256, 0, (hipStream_t)stream>>>(static_cast<const v4i*>(src), n16,
+                                                                                     static_cast<int*>(sink));
+    return (int)hipGetLastError();
 }

@@ -14,8 +14,9 @@
 // silu depends only on the 16-bit input, so it is checked exhaustively: on all 65,536 fp16 and all 65,536 bf16 inputs
 // the float32 result of this expression is within 2 float32 ulps of the one built on a correctly rounded exp and
 // rounds to the same 16-bit value (GPU test against the oracle's table).  For the same reason the SiLU kernel that
-// normally runs looks silu up in a table of the device's own 16-bit results for all 65,536 inputs, built once per
-// device with the expression above and held in LDS: bit-identical to evaluating it, at a third of the VALU work.
+// normally runs looks silu up in a table of all 65,536 16-bit results per type, generated at build time from the
+// correctly rounded definition (vllm_turing_amd/silu_table.py into silu_table.inc), compiled in as read-only device
+// data and held in LDS: the same 16-bit values as evaluating it, at a third of the VALU work, with no set-up.
 //
 // A third kernel fuses the residual add and the RMSNorm in front of the quantization (vLLM's
 // rms_norm_dynamic_per_token_quant as vllm_turing/tailoverlap.py:145 calls it): s = x + r (float), r <- RN_T(s),
@@ -23,8 +24,6 @@
 // ~1e-12), y = RN_T(float(RN_T(s * rms)) * w), scale = max(absmax(y) / 127, FLT_EPSILON), q = rint(y * (1 / scale)).
 #include <float.h>
 
-#include <atomic>
-#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -174,28 +173,25 @@ __global__ void __launch_bounds__(1024) silu_mul_quant_kernel(const uint16_t* __
     }
 }
 
-// silu of every 16-bit input pattern (test export: the exhaustive check of the device arithmetic).
-template <typename T>
-__global__ void silu_table_kernel(uint16_t* __restrict__ out) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < 65536) out[i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
-}
-
 // ---- SiLU * up + quant through a table of the 16-bit silu --------------------------------------------------------
-// silu is rounded to 16 bits before the product, so it is a function of the 16-bit gate pattern alone: the device
-// computes its value for all 65,536 patterns once (silu_lut_init_kernel: the same silu_f and rounding as the kernel
-// above, so the table kernel is bit-identical to it by construction), and a persistent block per CU copies the
-// 128 KB table of its dtype into LDS and looks the gate up.  ~12 VALU instructions per element instead of ~42, which
-// takes the kernel from VALU-bound to HBM-bound at prefill sizes.
-__device__ uint16_t g_silu_lut[2][65536];
-
-template <typename T>
-__global__ void __launch_bounds__(256) silu_lut_init_kernel() {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < 65536) g_silu_lut[std::is_same<T, bf16>::value ? DT_BF16 : DT_F16][i] = from_float<T>(silu_f(to_float(T{(uint16_t)i})));
-}
-
+// silu is rounded to 16 bits before the product, so it is a function of the 16-bit gate pattern alone: its value for
+// all 65,536 patterns of each type is generated at build time (silu_table.inc, fp16 first, then bf16), and a
+// persistent block per CU copies the 128 KB table of its dtype into LDS and looks the gate up.  ~12 VALU instructions
+// per element instead of ~42, which takes the kernel from VALU-bound to HBM-bound at prefill sizes.
 constexpr int LUT_ENTRIES = 65536;
+__device__ __align__(16) const uint16_t g_silu_lut[2][LUT_ENTRIES] = {
+#include "silu_table.inc"
+};
+
+// silu of every 16-bit input pattern (test export): dtype 0 / 1 the device's own arithmetic (the exhaustive check of
+// silu_f), 2 / 3 a copy of the compiled-in table of dtype 0 / 1.
+template <typename T>
+__global__ void silu_table_kernel(uint16_t* __restrict__ out, int table) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < LUT_ENTRIES)
+        out[i] = table ? g_silu_lut[std::is_same<T, bf16>::value ? DT_BF16 : DT_F16][i]
+                       : from_float<T>(silu_f(to_float(T{(uint16_t)i})));
+}
 
 // The table of dtype dt into LDS by direct-to-LDS loads: 128 loads of 1 KB shared out over the block's wavefronts,
 // all in flight at once (a plain device function: in a template the buffer-descriptor type drops the host stub).
@@ -510,35 +506,10 @@ static int run_ptq(const void* x, void* q, void* s, int M, int K, long ldx, hipS
     return 0;
 }
 
-// The silu tables are built on a device by the first call there that is not being captured into a graph, and
-// synchronised once, so that every stream of the device sees them; until then (and under capture) calls take the
-// direct kernel, as do rows longer than LUT_MAX_VPT vectors per thread.  The table kernel is as fast or faster at
-// every M (M=1 7.3 -> 5.5 us, M=511 15.2 -> 11.1 us, M=4096 -9% at I = 17408).
+// The table kernel takes every row of up to LUT_MAX_VPT vectors per thread; longer rows take the direct kernel.  The
+// table kernel is as fast or faster at every M (M=1 7.3 -> 5.5 us, M=511 15.2 -> 11.1 us, M=4096 -9% at I = 17408).
 constexpr int LUT_MAX_VPT = 5;                            // I <= 40960: two row buffers in registers, no spills
 enum : int { SMQ_ANY = 0, SMQ_DIRECT = 1, SMQ_TABLE = 2 };
-static std::atomic<int> g_lut_ready[64][2];
-static std::mutex g_lut_mu;
-
-static bool silu_lut_ready(int dt, hipStream_t st) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    if (g_lut_ready[dev][dt].load(std::memory_order_acquire)) return true;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-        (void)hipGetLastError();
-        return false;
-    }
-    std::lock_guard<std::mutex> lock(g_lut_mu);
-    if (g_lut_ready[dev][dt].load(std::memory_order_acquire)) return true;
-    if (dt == DT_F16) silu_lut_init_kernel<f16><<<LUT_ENTRIES / 256, 256, 0, st>>>();
-    else silu_lut_init_kernel<bf16><<<LUT_ENTRIES / 256, 256, 0, st>>>();
-    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    g_lut_ready[dev][dt].store(1, std::memory_order_release);
-    return true;
-}
 
 
 template <typename T, int VPT>
@@ -553,8 +524,7 @@ static void launch_smq_lut(const uint16_t* gp, int8_t* qp, float* sp, int M, int
 template <typename T>
 static int run_smq(const void* gu, void* q, void* s, int M, int I, hipStream_t st, int path = SMQ_ANY) {
     const int nvec = I / 8, lvpt = (nvec + 1023) / 1024;
-    const bool table_ok = lvpt <= LUT_MAX_VPT && path != SMQ_DIRECT &&
-                          silu_lut_ready(std::is_same<T, bf16>::value ? DT_BF16 : DT_F16, st);
+    const bool table_ok = lvpt <= LUT_MAX_VPT && path != SMQ_DIRECT;
     if (path == SMQ_TABLE && !table_ok) return 1;
     if (table_ok) {
         const int threads = ((nvec + lvpt - 1) / lvpt + 63) / 64 * 64;
@@ -658,19 +628,21 @@ extern "C" int silu_mul_quant_bf16(const void* gu, void* q, void* scales, int M,
 }
 
 // Test export: silu_mul_quant / silu_mul_quant_bf16 (dtype 0 / 1) through one kernel: path 1 the direct kernel, 2 the
-// table kernel (returns 1 where it does not apply: I > 40960, or its table not yet built under graph capture).
+// table kernel (returns 1 where it does not apply: I > 40960).
 extern "C" int silu_mul_quant_path(const void* gu, void* q, void* scales, int M, int I, int dtype, int path,
                                    void* stream) {
     if ((dtype != DT_F16 && dtype != DT_BF16) || (path != SMQ_DIRECT && path != SMQ_TABLE)) return 1;
     return smq_entry(gu, q, scales, M, I, dtype, stream, path);
 }
 
-// Test export: silu of all 65,536 input patterns of dtype into out[65536] (uint16 bit patterns).
+// Test export: silu of all 65,536 input patterns into out[65536] (uint16 bit patterns): dtype 0 / 1 computed by the
+// device (fp16 / bf16), 2 / 3 the compiled-in table the SiLU kernel looks up (fp16 / bf16).
 extern "C" int silu_table(void* out, int dtype, void* stream) {
-    if (!out || (dtype != DT_F16 && dtype != DT_BF16)) return -1;
+    if (!out || dtype < 0 || dtype > 3) return -1;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == DT_F16) silu_table_kernel<f16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out));
-    else silu_table_kernel<bf16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out));
+    const int table = dtype >= 2, dt = dtype & 1;
+    if (dt == DT_F16) silu_table_kernel<f16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out), table);
+    else silu_table_kernel<bf16><<<256, 256, 0, st>>>(static_cast<uint16_t*>(out), table);
     return (int)hipGetLastError();
 }
 

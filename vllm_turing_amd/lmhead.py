@@ -2,17 +2,21 @@
 scale per row (half the memory of fp16), logits from the MI355X kernel w8a16_gemv (csrc/gemm.hip: w8a16_kernel).
 
 The counterpart of vllm_turing/lmhead.py.  The reference routes up to 4 rows to its GEMV, 5..64 to a tensor-core
-kernel, 16-row GEMV passes up to 256 rows and chunked dequantisation above; here one MFMA kernel takes up to 32 rows
-per pass and every row count runs in passes of it, so no path leaves the HIP kernel.  VLLM_TURING_LMHEAD=0 disables
-install().
+kernel, 16-row GEMV passes up to 256 rows and chunked dequantisation above (lmhead.py:71-99).  Here the weight-
+streaming kernels take up to 32 rows per pass (the VALU kernel at one or two rows, the MFMA kernel above) and every
+row count up to GEMV_MAX_M runs in passes of them; above GEMV_MAX_M rows each pass would re-read the whole head, so,
+as the reference does, the head is dequantized DEQUANT_ROWS rows at a time ((w * s) rounded to the activation type)
+and multiplied with the library GEMM (the matmul is compute-bound there).  VLLM_TURING_LMHEAD=0 disables install().
 """
 import os
 
 import torch
 
-from . import _lib
+from . import _lib, hooks
 
 PASS_ROWS = 32          # rows per kernel launch
+GEMV_MAX_M = 256        # above this many rows: chunked dequantization and a library GEMM (lmhead.py:17,93-99)
+DEQUANT_ROWS = 4096     # head rows dequantized per chunk (lmhead.py:93)
 
 
 @torch.no_grad()
@@ -33,6 +37,18 @@ _hlib = torch.library.Library("vllm_turing_amd", "FRAGMENT")
 _hlib.define("w8a16_mm(Tensor x, Tensor w, Tensor s, Tensor? bias) -> Tensor")
 
 
+def _dequant_mm(x, w, s, bias, out):
+    """Rows above GEMV_MAX_M (vllm_turing/lmhead.py:93-99): out[:, chunk] = x @ RN_T(w[chunk] * s[chunk])^T, then
+    out += bias, with the chunk's weights dequantized on the device and the product on the library GEMM."""
+    N = w.shape[0]
+    for j in range(0, N, DEQUANT_ROWS):
+        wd = (w[j:j + DEQUANT_ROWS].float() * s[j:j + DEQUANT_ROWS, None]).to(x.dtype)
+        out[:, j:j + DEQUANT_ROWS] = torch.mm(x, wd.t().contiguous())
+    if bias is not None:
+        out += bias
+    return out
+
+
 def _w8a16_mm_hip(x, w, s, bias):
     M, K = x.shape
     N = w.shape[0]
@@ -40,6 +56,8 @@ def _w8a16_mm_hip(x, w, s, bias):
         raise ValueError(f"w8a16_mm takes float16 / bfloat16 activations, got {x.dtype}")
     x = x.contiguous()
     out = torch.empty(M, N, dtype=x.dtype, device=x.device)
+    if M > GEMV_MAX_M:
+        return _dequant_mm(x, w, s, bias, out)
     L = _lib.lib()
     code = _lib.dtype_code(x.dtype)
     st = _lib.stream_handle(x.device)
@@ -77,46 +95,57 @@ def w8a16_mm_rows(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, rows: torch
     L = _lib.lib()
     for r0 in range(0, M, PASS_ROWS):
         r1 = min(M, r0 + PASS_ROWS)
-        rc = L.w8a16_gemv_rows(x[r0:r1].data_ptr(), w.data_ptr(), s.data_ptr(),
-                               bias.data_ptr() if bias is not None else None, out[r0:r1].data_ptr(), r1 - r0, N, K,
-                               _lib.dtype_code(x.dtype), rows.data_ptr(), w.shape[0], _lib.stream_handle(x.device))
+        rc = L.w8a16_gemv_rows_bounded(x[r0:r1].data_ptr(), w.data_ptr(), s.data_ptr(),
+                                       bias.data_ptr() if bias is not None else None, out[r0:r1].data_ptr(), r1 - r0,
+                                       N, K, _lib.dtype_code(x.dtype), rows.data_ptr(), w.shape[0],
+                                       _lib.stream_handle(x.device))
         if rc != 0:
-            raise RuntimeError(f"w8a16_gemv_rows failed: {rc}")
+            raise RuntimeError(f"w8a16_gemv_rows_bounded failed: {rc}")
     return out
 
 
+def kernel_takes(n_rows: int, k: int) -> bool:
+    """Whether the weight-streaming kernels take an int8 head of n_rows x k (32-bit byte offsets into it)."""
+    return k % 16 == 0 and n_rows * k < 2 ** 31
+
+
+def _to_int8_head(layer):
+    """Swap a loaded head's 16-bit weight for int8 rows + float32 scales (layer.turing_w8 / turing_s), freeing it."""
+    w16 = layer.weight.data
+    layer.turing_w8, layer.turing_s = quantize_rows(w16)
+    layer.weight.data = w16.new_empty(0, w16.shape[1])
+    del w16
+    torch.cuda.empty_cache()
+
+
 def install():
-    """After weight loading, replace vLLM's ParallelLMHead weight by int8 rows + scales and compute its logits with
-    w8a16_mm (vllm_turing/lmhead.py:104-141), when vLLM is importable on a gfx950 device."""
+    """Give vLLM's unquantized LM head an int8 weight after loading and compute its logits with w8a16_mm, when vLLM
+    is importable on a gfx950 device (vllm_turing/lmhead.py:104-141 does this on sm75).  Heads the kernels cannot
+    address (N * K >= 2^31) keep their 16-bit weight and vLLM's own apply()."""
     if os.environ.get("VLLM_TURING_LMHEAD", "1") == "0":
         return False
     try:
         from vllm.model_executor.layers import vocab_parallel_embedding as vpe
     except ImportError:
         return False
-    if not torch.cuda.is_available() or "gfx950" not in torch.cuda.get_device_properties(0).gcnArchName:
+    if not hooks.on_gfx950():
         return False
-    M = vpe.UnquantizedEmbeddingMethod
-    if getattr(M, "_vllm_turing_lmhead", False):
+    method = vpe.UnquantizedEmbeddingMethod
+    vllm_load, vllm_apply = method.process_weights_after_loading, method.apply
+    if hooks.ours(vllm_load) and hooks.ours(vllm_apply):
         return True
-    orig_pw, orig_apply = M.process_weights_after_loading, M.apply
 
     def process_weights_after_loading(self, layer):
-        orig_pw(self, layer)
-        if isinstance(layer, vpe.ParallelLMHead) and not hasattr(layer, "turing_w8") and layer.weight.dim() == 2 \
-                and layer.weight.is_cuda and layer.weight.shape[1] % 16 == 0:
-            w = layer.weight.data
-            layer.turing_w8, layer.turing_s = quantize_rows(w)
-            layer.weight.data = torch.empty(0, w.shape[1], dtype=w.dtype, device=w.device)   # free the 16-bit head
-            del w
-            torch.cuda.empty_cache()
+        vllm_load(self, layer)
+        w = layer.weight
+        if isinstance(layer, vpe.ParallelLMHead) and not hasattr(layer, "turing_w8") and w.dim() == 2 \
+                and w.is_cuda and kernel_takes(*w.shape):
+            _to_int8_head(layer)
 
     def apply(self, layer, x, bias=None):
-        if hasattr(layer, "turing_w8"):
-            return w8a16_mm(x, layer.turing_w8, layer.turing_s, bias)
-        return orig_apply(self, layer, x, bias)
+        if not hasattr(layer, "turing_w8"):
+            return vllm_apply(self, layer, x, bias)
+        return w8a16_mm(x, layer.turing_w8, layer.turing_s, bias)
 
-    M.process_weights_after_loading = process_weights_after_loading
-    M.apply = apply
-    M._vllm_turing_lmhead = True
-    return True
+    hooks.replace(method, "process_weights_after_loading", process_weights_after_loading)
+    return hooks.replace(method, "apply", apply)

@@ -17,7 +17,7 @@ import os
 
 import torch
 
-from . import _lib
+from . import _lib, hooks
 
 ENABLED = os.environ.get("VLLM_TURING_NORMQUANT", "1") != "0"
 
@@ -75,35 +75,29 @@ def rms_norm_dynamic_per_token_quant(input: torch.Tensor, weight: torch.Tensor, 
     return q.reshape(shape), s
 
 
-rms_norm_dynamic_per_token_quant._vllm_turing = True
-
-
 def gemma_weight(w: torch.Tensor) -> torch.Tensor:
     """The GemmaRMSNorm weight the fused op takes: 1 + w in float32, back to w's dtype (tailoverlap.py:123)."""
     return (1.0 + w.float()).to(w.dtype)
 
 
 def install():
-    """Route vllm._custom_ops.rms_norm_dynamic_per_token_quant's int8 case to the HIP kernel when vLLM is importable
-    (other output types keep vLLM's op)."""
+    """Route vllm._custom_ops.rms_norm_dynamic_per_token_quant's int8 case to the HIP kernel (other output types keep
+    vLLM's op) when vLLM is importable on a gfx950 device."""
     if not ENABLED:
         return False
     try:
         from vllm import _custom_ops as ops
     except ImportError:
         return False
-    orig = getattr(ops, "rms_norm_dynamic_per_token_quant", None)
-    if orig is None:
+    vllm_op = getattr(ops, "rms_norm_dynamic_per_token_quant", None)
+    if vllm_op is None or not hooks.on_gfx950():
         return False
-    if getattr(orig, "_vllm_turing", False):
+    if hooks.ours(vllm_op):
         return True
 
-    def hooked(input, weight, epsilon, quant_dtype, scale_ub=None, residual=None):
+    def rms_norm_dynamic_per_token_quant_hook(input, weight, epsilon, quant_dtype, scale_ub=None, residual=None):
         if quant_dtype == torch.int8:
             return rms_norm_dynamic_per_token_quant(input, weight, epsilon, quant_dtype, scale_ub, residual)
-        return orig(input, weight, epsilon, quant_dtype, scale_ub, residual)
+        return vllm_op(input, weight, epsilon, quant_dtype, scale_ub, residual)
 
-    hooked._vllm_turing = True
-    hooked._orig = orig
-    ops.rms_norm_dynamic_per_token_quant = hooked
-    return True
+    return hooks.replace(ops, "rms_norm_dynamic_per_token_quant", rms_norm_dynamic_per_token_quant_hook)

@@ -17,7 +17,7 @@ import os
 
 import torch
 
-from . import _lib
+from . import _lib, hooks
 
 ENABLED = os.environ.get("VLLM_TURING_QUANTFUSE", "1") != "0"
 
@@ -74,29 +74,45 @@ def scaled_int8_quant(input, scale=None, azp=None, symmetric=True):
     raise NotImplementedError("only dynamic symmetric per-token quantization is implemented (the W8A8 path)")
 
 
-scaled_int8_quant._vllm_turing = True
-
-
 def install():
-    """Route vllm._custom_ops.scaled_int8_quant's dynamic symmetric case to the HIP kernel when vLLM is importable
-    (other cases keep vLLM's op), as vllm_turing/quantfuse.py:27-43 does for its compiled case."""
+    """Route vllm._custom_ops.scaled_int8_quant's dynamic symmetric case to the HIP kernel (other cases keep vLLM's
+    op) when vLLM is importable on a gfx950 device.  The reference takes over that case only while torch.compile
+    traces, so that inductor fuses its torch formula into the producer (vllm_turing/quantfuse.py:27-43); without a
+    Triton path here, eager and compiled calls alike run the kernel through the opaque op.  As there, the compile cache
+    key is extended so a graph traced without the hook is not reused with it (quantfuse.py:45-55)."""
     if not ENABLED:
         return False
     try:
         from vllm import _custom_ops as ops
     except ImportError:
         return False
-    if getattr(ops.scaled_int8_quant, "_vllm_turing", False):
+    if not hooks.on_gfx950():
+        return False
+    vllm_op = ops.scaled_int8_quant
+    if hooks.ours(vllm_op):
         return True
-    orig = ops.scaled_int8_quant
 
-    def hooked(input, scale=None, azp=None, symmetric=True):
+    def scaled_int8_quant_hook(input, scale=None, azp=None, symmetric=True):
         if scale is None and azp is None and symmetric:
             q, s = per_token_quant(input)
             return q, s, None
-        return orig(input, scale, azp, symmetric)
+        return vllm_op(input, scale, azp, symmetric)
 
-    hooked._vllm_turing = True
-    hooked._orig = orig
-    ops.scaled_int8_quant = hooked
+    hooks.replace(ops, "scaled_int8_quant", scaled_int8_quant_hook)
+    _extend_compile_cache_key()
     return True
+
+
+def _extend_compile_cache_key():
+    try:
+        from vllm.compilation import caching
+    except ImportError:
+        return
+    factors = getattr(caching, "aot_compile_hash_factors", None)
+    if factors is None or hooks.ours(factors):
+        return
+
+    def aot_compile_hash_factors(vllm_config):
+        return [*factors(vllm_config), "vllm_turing_amd.per_token_quant"]
+
+    hooks.replace(caching, "aot_compile_hash_factors", aot_compile_hash_factors)

@@ -21,7 +21,7 @@ import os
 
 import torch
 
-from . import _lib
+from . import _lib, hooks
 
 MAX_M = int(os.environ.get("VLLM_TURING_GEMV_MAX_M", "12"))
 MMA_MAX_M = min(int(os.environ.get("VLLM_TURING_MMA_MAX_M", "32")), 32)
@@ -165,19 +165,13 @@ def cutlass_scaled_mm(a, b, scale_a, scale_b, out_dtype, bias=None):
     return out.view(*target_shape)
 
 
-cutlass_scaled_mm._vllm_turing = True
-
-
 def install():
-    """Replace vllm._custom_ops.cutlass_scaled_mm when vLLM is importable and the device is gfx950
-    (vllm_turing/w8a8.py:125-150 gates on sm75)."""
+    """Route vllm._custom_ops.cutlass_scaled_mm to cutlass_scaled_mm above when vLLM is importable and the device is
+    gfx950 (the reference replaces the same function on sm75, vllm_turing/w8a8.py:125-150)."""
     try:
         from vllm import _custom_ops as ops
     except ImportError:
         return False
-    if getattr(ops.cutlass_scaled_mm, "_vllm_turing", False):
-        return True
-    if not torch.cuda.is_available() or "gfx950" not in torch.cuda.get_device_properties(0).gcnArchName:
+    if not hooks.on_gfx950():
         return False
-    ops.cutlass_scaled_mm = cutlass_scaled_mm
-    return True
+    return hooks.replace(ops, "cutlass_scaled_mm", cutlass_scaled_mm)
