@@ -47,13 +47,12 @@ def test_smoothing_preserves_products():
              P + "mlp.gate_up_proj": d(H).abs() * 7, P + "mlp.down_proj": d(I).abs() * 2,
              P + "linear_attn.out_proj": d(n_vh * vhd).abs() * 4}
     stats = {k: v.float() for k, v in stats.items()}
-    wmax = {c: t[c].float().abs().amax(dim=0) for grp in ck.smoothing_groups(stats) for c in grp[1] if c in t}
-    plan = ck.smoothing_plan(stats, wmax, tc, 0.5)
-    sm = {k: (ck.apply_smoothing(k, v, plan) if ck.apply_smoothing(k, v, plan) is not None else v.float()).double()
-          for k, v in t.items()}
+    wmax = {c: t[c].float().abs().amax(dim=0) for c in ck.Smoothing.consumers(stats) if c in t}
+    plan = ck.Smoothing.plan(stats, wmax, tc, 0.5)
+    sm = {k: (plan.apply(k, v) if plan.apply(k, v) is not None else v.float()).double() for k, v in t.items()}
     x, z = d(T, H), d(T, n_vh * vhd)
     # qkv after the input norm (v's rows also carry the o_proj group's 1 / s: its outputs are scaled per channel)
-    s_o = plan[1][P + "self_attn.v_proj.weight"].double()
+    s_o = plan.edits[P + "self_attn.v_proj.weight"].rows.double()
     for proj in ("q_proj", "k_proj", "v_proj"):
         a = _rms_zc(x, t[P + "input_layernorm.weight"]) @ t[P + f"self_attn.{proj}.weight"].T
         b = _rms_zc(x, sm[P + "input_layernorm.weight"]) @ sm[P + f"self_attn.{proj}.weight"].T
@@ -84,7 +83,7 @@ def test_smoothing_preserves_products():
         return n.reshape(T, n_vh * vhd) @ tt[P + "linear_attn.out_proj.weight"].T
     assert torch.allclose(gdn(t), gdn(sm), rtol=1e-5, atol=1e-5)
     # the factors themselves: s = x^a / w^(1-a), clamped
-    s = plan[0][P + "mlp.down_proj.weight"]
+    s = plan.edits[P + "mlp.down_proj.weight"].cols
     ref = (stats[P + "mlp.down_proj"].clamp(min=1e-5) ** 0.5 / wmax[P + "mlp.down_proj.weight"].clamp(min=1e-5) ** 0.5)
     assert torch.allclose(s, ref.clamp(1e-2, 1e2))
 
@@ -100,6 +99,18 @@ def test_calibration_merge(tmp_path):
     st = ck.load_calibration(str(tmp_path))
     assert st["model.language_model.layers.0.mlp.down_proj"].tolist() == [1.0, 2.0, 3.0, 4.0]   # K shards in order
     assert st["model.language_model.layers.0.mlp.gate_up_proj"].tolist() == [2.0, 5.0, 3.0]     # max over ranks
+    assert len(st) == 2
+    # the MTP draft layers' files (rank<r>_m1, module names model.layers.<i>) merge into mtp.layers.<i>
+    m0 = {"model.layers.0.self_attn.o_proj": torch.tensor([7.0]), "model.layers.0.self_attn.qkv_proj": torch.tensor([1.0, 9.0])}
+    m1 = {"model.layers.0.self_attn.o_proj": torch.tensor([8.0]), "model.layers.0.self_attn.qkv_proj": torch.tensor([4.0, 2.0])}
+    torch.save(m0, str(tmp_path / "rank0_m1.pt"))
+    torch.save(m1, str(tmp_path / "rank1_m1.pt"))
+    st = ck.load_calibration(str(tmp_path))
+    assert st["mtp.layers.0.self_attn.o_proj"].tolist() == [7.0, 8.0]
+    assert st["mtp.layers.0.self_attn.qkv_proj"].tolist() == [4.0, 9.0]
+    assert st["model.language_model.layers.0.mlp.down_proj"].tolist() == [1.0, 2.0, 3.0, 4.0]
+    with pytest.raises(FileNotFoundError):
+        ck.load_calibration(str(tmp_path / "missing_dir_is_not_a_file"))
 
 
 def _tiny_model(d, smooth=False):
@@ -192,3 +203,52 @@ def test_load_rejects_other_formats(tmp_path):
     _tiny_model(str(d))
     with pytest.raises(ValueError):
         ck.load(str(d), device="cpu")
+
+
+def test_convert_folds_mtp_layers(tmp_path):
+    """Calibration directories carry the MTP draft layers' maxima in rank<r>_m1 files: the fold reaches mtp.layers.*
+    (its norm stored float32, its q / k / v quantized from the smoothed weights), exactly as a hand-applied fold."""
+    from safetensors.torch import save_file
+    src, dst, cal = tmp_path / "src", tmp_path / "dst", tmp_path / "calib"
+    src.mkdir()
+    cal.mkdir()
+    t = _tiny_model(str(src))
+    g = torch.Generator().manual_seed(6)
+    H = 64
+    P = "mtp.layers.0."
+    extra = {P + "self_attn.q_proj.weight": (torch.randn(64, H, generator=g) * 0.05).to(torch.bfloat16),
+             P + "self_attn.k_proj.weight": (torch.randn(32, H, generator=g) * 0.05).to(torch.bfloat16),
+             P + "self_attn.v_proj.weight": (torch.randn(32, H, generator=g) * 0.05).to(torch.bfloat16),
+             P + "input_layernorm.weight": (torch.randn(H, generator=g) * 0.05).to(torch.bfloat16)}
+    save_file(extra, str(src / "model-mtp.safetensors"), metadata={"format": "pt"})
+    idx = json.load(open(src / "model.safetensors.index.json"))
+    idx["weight_map"].update({n: "model-mtp.safetensors" for n in extra})
+    json.dump(idx, open(src / "model.safetensors.index.json", "w"))
+    main = {"language_model.model.layers.0.mlp.down_proj": torch.rand(48, generator=g) * 8}
+    save_file(main, str(cal / "rank0.safetensors"))
+    save_file({"language_model.model.layers.0.mlp.down_proj": torch.rand(48, generator=g) * 8},
+              str(cal / "rank1.safetensors"))
+    xm = [torch.rand(H, generator=g) * 8 for _ in range(2)]
+    for r in range(2):
+        torch.save({"model.layers.0.self_attn.qkv_proj": xm[r]}, str(cal / f"rank{r}_m1.pt"))
+    ck.convert(str(src), str(dst), "cpu", str(cal), 0.5, log=lambda *a: None)
+    from safetensors import safe_open
+    with safe_open(str(dst / "model-mtp.safetensors"), framework="pt") as f:
+        got = {n: f.get_tensor(n) for n in f.keys()}
+    x = torch.maximum(xm[0], xm[1])
+    w = torch.stack([extra[P + f"self_attn.{c}_proj.weight"].float().abs().amax(0) for c in "qkv"]).amax(0)
+    s = ck.smoothing_factors(x, w, 0.5)
+    assert torch.equal(got[P + "input_layernorm.weight"], (1 + extra[P + "input_layernorm.weight"].float()) / s - 1)
+    for c in "qkv":
+        q, sc = ck.quantize_per_channel(extra[P + f"self_attn.{c}_proj.weight"].float() * s[None, :])
+        assert torch.equal(got[P + f"self_attn.{c}_proj.weight"], q)
+        assert torch.equal(got[P + f"self_attn.{c}_proj.weight_scale"], sc)
+
+
+def test_cli(tmp_path, capsys):
+    src, dst = tmp_path / "src", tmp_path / "dst"
+    src.mkdir()
+    _tiny_model(str(src))
+    assert ck.main([str(src), str(dst), "cpu"]) == 0
+    out = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    assert out["quantized"] == 10 and out["max_rel_err"] < 0.02

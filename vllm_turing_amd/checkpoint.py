@@ -1,24 +1,32 @@
-"""compressed-tensors int-quantized W8A8 checkpoints: conversion from a bf16 safetensors model and loading into
+"""compressed-tensors int-quantized W8A8 checkpoints: conversion from a bf16 safetensors model, and loading into
 W8A8Linear layers (the data format on the input side of the W8A8 path).
 
-The format and the conversion arithmetic are the reference converter's (scripts/w8a8_convert.py), which vLLM's
-compressed-tensors loader reads:
-  * every quantized linear `<name>.weight` becomes int8 [N, K] plus `<name>.weight_scale` float32 [N, 1], symmetric
-    per output channel: scale = max(amax(|w_row|), 1e-12) / 127, q = clamp(round_half_even(w / scale), -128, 127)
-    (:165-178); activations are quantized per token at run time (config only);
-  * config.json gains quantization_config {quant_method compressed-tensors, format int-quantized, config_groups.group_0
-    (8-bit symmetric per-channel static weights, 8-bit symmetric per-token dynamic inputs), ignore list} (:209-231);
-  * shards keep the source's layout; model.safetensors.index.json is rewritten; other files are copied (:199-206);
-  * optional SmoothQuant fold (:60-149): per group of linears sharing one input X, per input channel j,
-    s_j = clamp(max|X_j|^a / max|W_j|^(1-a), 1e-2, 1e2); consumers get W[:, j] * s_j; the producer of X absorbs 1 / s_j
-    (zero-centred RMSNorm weight (1 + w) / s - 1, plain norm weight w / s, or the rows of the producing linear / s);
-    changed unquantized tensors are stored float32.
-Which tensors are quantized, which stay as stored, and the calibration-file merge rule are the reference's, kept
-alike because they define the checkpoint a vLLM deployment of the reference loads.
+On-disk format (the one vLLM's compressed-tensors loader reads, as the reference converter writes it:
+scripts/w8a8_convert.py:51-53,165-178,209-231):
+  * each quantized linear `<name>.weight` is int8 [N, K] with `<name>.weight_scale` float32 [N, 1], symmetric per
+    output channel: scale = max(amax |w_row|, 1e-12) / 127, q = clamp(round_half_even(w / scale), -128, 127);
+    activations are quantized per token at run time (configuration only);
+  * config.json carries quantization_config (compressed-tensors, int-quantized, one config group of 8-bit symmetric
+    per-channel static weights and 8-bit symmetric per-token dynamic inputs, and the ignore list);
+  * the source's shard layout is kept, the index rewritten, the other files copied.
+QUANT_PATTERN, IGNORE and quantization_config() are that format and stay as the reference has them.
 
-Command line: python -m vllm_turing_amd.checkpoint <src dir> <dst dir> [device] [--smooth <calibration file or dir>]
-[--alpha a].  Conversion runs with torch on `device` (a GPU by default when one is present, else the CPU).
+Conversion, as this module organises it: a SourceModel reads the source shards one at a time (the model never sits in
+memory whole); an optional Smoothing maps tensor names to Edits; convert_tensor turns one source tensor into the
+tensors stored for it; write_shard / finish write the output.  The SmoothQuant fold (scripts/w8a8_convert.py:60-149):
+for each group of linears sharing one input X (SMOOTH_GROUPS, a table of the model's structure), per input channel j,
+  s_j = clamp(max(max|X_j|, 1e-5)^a / max(max|W_j|, 1e-5)^(1-a), 1e-2, 1e2),
+the group's weights take W[:, j] * s_j and the producer of X absorbs 1 / s_j: a zero-centred RMSNorm weight becomes
+(1 + w) / s - 1, a plain norm weight w / s, a producing linear's output rows W[j, :] / s_j.  Where one factor must
+serve several channels (o_proj after GQA v heads; the GDN gated norm shared by the value heads) the maxima are pooled
+over those channels first.  Smoothed tensors that stay unquantized are stored float32.  The calibration maxima come
+from per-rank files (main model `rank<r>`, MTP draft layers `rank<r>_m1`); row-parallel layers' shards are
+concatenated in rank order, the others reduced with max (scripts/w8a8_convert.py:71-82).
+
+Command line: python -m vllm_turing_amd.checkpoint SRC DST [DEVICE] [--smooth CALIB] [--alpha A]
 """
+import argparse
+import dataclasses
 import json
 import os
 import re
@@ -29,18 +37,16 @@ import torch
 
 from .linear import W8A8Linear
 
-# the linears that become int8 (scripts/w8a8_convert.py:55-57)
+# ---- the on-disk format (scripts/w8a8_convert.py:51-53,209-231) -----------------------------------------------------
 QUANT_PATTERN = re.compile(
     r"^(model\.language_model\.layers\.\d+\.(linear_attn\.(in_proj_qkv|in_proj_z|out_proj)"
     r"|self_attn\.(q_proj|k_proj|v_proj|o_proj)|mlp\.(gate_proj|up_proj|down_proj))"
     r"|mtp\.layers\.\d+\.(self_attn\.(q_proj|k_proj|v_proj|o_proj)|mlp\.(gate_proj|up_proj|down_proj)))\.weight$")
-# kept as stored (scripts/w8a8_convert.py:224-226)
 IGNORE = ["lm_head", "re:.*visual.*", "re:.*conv1d.*", "re:.*mtp\\.fc.*", "re:.*linear_attn\\.in_proj_(a|b)$"]
-ROW_PARALLEL = ("o_proj", "down_proj", "out_proj")      # calibration stats of these are K shards in rank order
 
 
 def quantization_config():
-    """The quantization_config block written into config.json (scripts/w8a8_convert.py:209-231)."""
+    """The quantization_config block of config.json."""
     return {
         "quant_method": "compressed-tensors",
         "format": "int-quantized",
@@ -67,197 +73,300 @@ def quantize_per_channel(w: torch.Tensor):
     """float weight [N, K] -> (int8 [N, K], float32 scale [N, 1]): symmetric per output channel."""
     wf = w.to(torch.float32)
     scale = wf.abs().amax(dim=1, keepdim=True).clamp(min=1e-12) / 127.0
-    q = torch.round(wf / scale).clamp(-128, 127).to(torch.int8)
-    return q, scale
+    return torch.round(wf / scale).clamp(-128, 127).to(torch.int8), scale
 
 
-def smoothing_factors(x_absmax: torch.Tensor, w_absmax: torch.Tensor, alpha: float):
-    """s_j = clamp(max|X_j|^alpha / max|W_j|^(1 - alpha), 1e-2, 1e2) (both maxima floored at 1e-5)."""
-    return (x_absmax.clamp(min=1e-5) ** alpha / w_absmax.clamp(min=1e-5) ** (1 - alpha)).clamp(1e-2, 1e2)
+# ---- calibration maxima ------------------------------------------------------------------------------------------------
+# The model's module names in the calibration files, per file tag, and the checkpoint prefix they stand for: the main
+# model's decoder layers, and (tag _m1) the MTP draft layers, which the draft model names model.layers.<i>.
+CALIB_TAGS = {"": ("language_model.model.layers.", "model.language_model.layers."),
+              "_m1": ("model.layers.", "mtp.layers.")}
+ROW_PARALLEL = ("o_proj", "down_proj", "out_proj")   # their activation maxima are K shards, one per rank
 
 
-def _load_stats_file(path):
+def _read_stats(path):
     if path.endswith(".safetensors"):
         from safetensors.torch import load_file
         return load_file(path)
     return torch.load(path, map_location="cpu", weights_only=True)
 
 
-def _checkpoint_name(module_name, tag):
-    """vLLM module name -> checkpoint tensor prefix (scripts/w8a8_convert.py:76-77): the language model's layers, or
-    for a draft-model file (tag "_m1") the MTP layers."""
-    if tag:
-        return module_name.replace("model.layers.", "mtp.layers.", 1)
-    return module_name.replace("language_model.model.layers.", "model.language_model.layers.", 1)
-
-
-def load_calibration(path, tag=""):
-    """Per-input-channel activation maxima {checkpoint module name: float32 [K]}.  `path` is one file ({name:
-    tensor}) or a directory of per-rank files rank<r><tag>.pt / .safetensors as the reference's calibration hooks
-    write them (vllm_turing/calib.py), merged as its converter does: row-parallel layers' K shards concatenated in rank
-    order, the others reduced with max.  Module names are mapped to checkpoint names."""
-    if os.path.isfile(path):
-        return {_checkpoint_name(k, tag): v.float() for k, v in _load_stats_file(path).items()}
-    parts, r = [], 0
+def _rank_files(path, tag):
+    files = []
     while True:
-        f = next((os.path.join(path, f"rank{r}{tag}{ext}") for ext in (".safetensors", ".pt")
-                  if os.path.exists(os.path.join(path, f"rank{r}{tag}{ext}"))), None)
-        if f is None:
-            break
-        parts.append(_load_stats_file(f))
-        r += 1
-    if not parts:
-        raise FileNotFoundError(f"no rank<r>{tag} calibration files in {path}")
-    out = {}
-    for k in parts[0]:
-        if k.rsplit(".", 1)[1] in ROW_PARALLEL:
-            v = torch.cat([p[k] for p in parts]).float()
-        else:
-            v = torch.stack([p[k].float() for p in parts]).amax(dim=0)
-        out[_checkpoint_name(k, tag)] = v
-    return out
+        found = [os.path.join(path, f"rank{len(files)}{tag}{ext}") for ext in (".safetensors", ".pt")]
+        found = [f for f in found if os.path.exists(f)]
+        if not found:
+            return files
+        files.append(found[0])
 
 
-def smoothing_groups(stats):
-    """(stats key, consumer weight names, producer tensor name, producer kind, reduction) per linear group sharing one
-    input (scripts/w8a8_convert.py:85-101): the stats keys are module names …layers.<i>.self_attn.qkv_proj,
-    …mlp.gate_up_proj, …mlp.down_proj, …self_attn.o_proj, …linear_attn.in_proj_qkvz, …linear_attn.out_proj."""
-    groups = []
-    for k in stats:
-        p, role = k.rsplit(".", 1)
-        blk = p.rsplit(".", 1)[0] + "."
-        if role == "qkv_proj":
-            groups.append((k, [f"{p}.{c}.weight" for c in ("q_proj", "k_proj", "v_proj")],
-                           blk + "input_layernorm.weight", "zc", None))
-        elif role == "in_proj_qkvz":
-            groups.append((k, [f"{p}.{c}.weight" for c in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b")],
-                           blk + "input_layernorm.weight", "zc", None))
-        elif role == "gate_up_proj":
-            groups.append((k, [f"{p}.gate_proj.weight", f"{p}.up_proj.weight"],
-                           blk + "post_attention_layernorm.weight", "zc", None))
-        elif role == "down_proj":
-            groups.append((k, [f"{p}.down_proj.weight"], f"{p}.up_proj.weight", "rows", None))
-        elif role == "o_proj":
-            groups.append((k, [f"{p}.o_proj.weight"], f"{p}.v_proj.weight", "rows", "gqa"))
-        elif role == "out_proj":
-            groups.append((k, [f"{p}.out_proj.weight"], f"{p}.norm.weight", "plain", "heads"))
-    return groups
+def _merge_ranks(parts):
+    """{module: maxima} of every rank -> one dict: row-parallel modules concatenated in rank order, others max."""
+    merged = {}
+    for name in parts[0]:
+        vals = [p[name].float() for p in parts]
+        merged[name] = torch.cat(vals) if name.rsplit(".", 1)[-1] in ROW_PARALLEL else torch.stack(vals).amax(0)
+    return merged
 
 
-def smoothing_plan(stats, weight_absmax, text_config, alpha):
-    """(col_scale, row_scale, norm_fix): tensor name -> s for consumer columns (*), producer rows (/), producer norm
-    weights ((s, "zc" | "plain")).  weight_absmax maps consumer weight names to their per-input-channel max |W|."""
-    n_q, n_kv, hd = (text_config.get(k) for k in ("num_attention_heads", "num_key_value_heads", "head_dim"))
-    n_vh, vhd = text_config.get("linear_num_value_heads"), text_config.get("linear_value_head_dim")
-    col_scale, row_scale, norm_fix = {}, {}, {}
-    for k, cons, prod, kind, red in smoothing_groups(stats):
-        cons = [c for c in cons if c in weight_absmax]
-        if not cons:
+def load_calibration(path):
+    """Per-input-channel activation maxima {checkpoint module name: float32 [K]}.
+
+    path: one file of {module name: maxima} (main-model names), or a directory of per-rank files rank<r>.pt /
+    rank<r>.safetensors (main model) and rank<r>_m1.* (MTP draft layers), as the calibration hooks write them."""
+    if os.path.isfile(path):
+        old, new = CALIB_TAGS[""]
+        return {k.replace(old, new, 1): v.float() for k, v in _read_stats(path).items()}
+    stats = {}
+    for tag, (old, new) in CALIB_TAGS.items():
+        files = _rank_files(path, tag)
+        if not files:
+            if tag == "":
+                raise FileNotFoundError(f"no rank<r> calibration files in {path}")
             continue
-        w = torch.stack([weight_absmax[c] for c in cons]).amax(dim=0)
-        x = stats[k].float()
-        if red == "gqa":        # o_proj input channel h * hd + d belongs to v head h // (n_q / n_kv)
-            x = x.view(n_kv, n_q // n_kv, hd).amax(dim=1)
-            w = w.view(n_kv, n_q // n_kv, hd).amax(dim=1)
-        elif red == "heads":    # the gated norm's weight is per dimension, shared by all value heads
-            x = x.view(n_vh, vhd).amax(dim=0)
-            w = w.view(n_vh, vhd).amax(dim=0)
-        s = smoothing_factors(x, w, alpha)
-        if red == "gqa":
-            s_cols, s_prod = s.repeat_interleave(n_q // n_kv, dim=0).flatten(), s.flatten()
-        elif red == "heads":
-            s_cols, s_prod = s.repeat(n_vh), s
-        else:
-            s_cols = s_prod = s
-        for c in cons:
-            col_scale[c] = s_cols
-        if kind == "rows":
-            row_scale[prod] = s_prod
-        else:
-            norm_fix[prod] = (s_prod, kind)
-    return col_scale, row_scale, norm_fix
+        for k, v in _merge_ranks([_read_stats(f) for f in files]).items():
+            stats[k.replace(old, new, 1)] = v
+    return stats
 
 
-def apply_smoothing(name, t, plan, device="cpu"):
-    """The smoothed float32 tensor, or None if the plan leaves `name` untouched."""
-    col_scale, row_scale, norm_fix = plan
-    if name not in col_scale and name not in row_scale and name not in norm_fix:
-        return None
-    w = t.to(device, torch.float32)
-    if name in col_scale:
-        w = w * col_scale[name].to(device)[None, :]
-    if name in row_scale:
-        w = w / row_scale[name].to(device)[:, None]
-    if name in norm_fix:
-        s, kind = norm_fix[name]
-        s = s.to(device)
-        w = (1 + w) / s - 1 if kind == "zc" else w / s
-    return w
+# ---- SmoothQuant -------------------------------------------------------------------------------------------------------
+@dataclasses.dataclass(frozen=True)
+class SmoothGroup:
+    """Linears that read one activation, named relative to their decoder layer's prefix.
+
+    module: the calibrated module whose input maxima the group uses; consumers: the weights that read that input;
+    producer: the tensor that writes it; fold: how the producer absorbs 1 / s ("zero_centred_norm", "norm", "rows");
+    pooling: channels that must share one factor ("none", "kv_head" for o_proj over GQA v heads, "head_dim" for the
+    GDN gated norm whose weight is per dimension and shared by the value heads)."""
+    module: str
+    consumers: tuple
+    producer: str
+    fold: str
+    pooling: str = "none"
+
+
+SMOOTH_GROUPS = (
+    SmoothGroup("self_attn.qkv_proj", ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight"),
+                "input_layernorm.weight", "zero_centred_norm"),
+    SmoothGroup("linear_attn.in_proj_qkvz", ("linear_attn.in_proj_qkv.weight", "linear_attn.in_proj_z.weight",
+                                             "linear_attn.in_proj_a.weight", "linear_attn.in_proj_b.weight"),
+                "input_layernorm.weight", "zero_centred_norm"),
+    SmoothGroup("mlp.gate_up_proj", ("mlp.gate_proj.weight", "mlp.up_proj.weight"), "post_attention_layernorm.weight",
+                "zero_centred_norm"),
+    SmoothGroup("mlp.down_proj", ("mlp.down_proj.weight",), "mlp.up_proj.weight", "rows"),
+    SmoothGroup("self_attn.o_proj", ("self_attn.o_proj.weight",), "self_attn.v_proj.weight", "rows", "kv_head"),
+    SmoothGroup("linear_attn.out_proj", ("linear_attn.out_proj.weight",), "linear_attn.norm.weight", "norm",
+                "head_dim"),
+)
+_GROUP_BY_MODULE = {g.module: g for g in SMOOTH_GROUPS}
+_LAYER = re.compile(r"^(.*\.layers\.\d+\.)(.+)$")
+
+
+def smoothing_factors(x_absmax: torch.Tensor, w_absmax: torch.Tensor, alpha: float):
+    """s_j = clamp(max(x_j, 1e-5)^alpha / max(w_j, 1e-5)^(1 - alpha), 1e-2, 1e2)."""
+    return (x_absmax.clamp(min=1e-5) ** alpha / w_absmax.clamp(min=1e-5) ** (1 - alpha)).clamp(1e-2, 1e2)
+
+
+def _groups_in(stats):
+    """(layer prefix, SmoothGroup) for every calibrated module that heads a group."""
+    for key in stats:
+        m = _LAYER.match(key)
+        if m and m.group(2) in _GROUP_BY_MODULE:
+            yield m.group(1), _GROUP_BY_MODULE[m.group(2)]
+
+
+class _Heads:
+    """The head geometry the pooled groups need, from the model's text config."""
+
+    def __init__(self, text_config):
+        c = text_config
+        self.n_q, self.n_kv, self.hd = c.get("num_attention_heads"), c.get("num_key_value_heads"), c.get("head_dim")
+        self.n_vh, self.vhd = c.get("linear_num_value_heads"), c.get("linear_value_head_dim")
+
+    def pool(self, v, pooling):
+        """Per-channel maxima -> one value per shared factor (max over the channels that share it)."""
+        if pooling == "kv_head":          # o_proj input channel (q head h, d) reads v head h // (n_q / n_kv)
+            return v.view(self.n_kv, self.n_q // self.n_kv, self.hd).amax(dim=1)
+        if pooling == "head_dim":         # value head h, dimension d share the norm weight of d
+            return v.view(self.n_vh, self.vhd).amax(dim=0)
+        return v
+
+    def spread(self, s, pooling):
+        """Factors per shared slot -> (factor per consumer input column, factor per producer element)."""
+        if pooling == "kv_head":
+            return s.repeat_interleave(self.n_q // self.n_kv, dim=0).reshape(-1), s.reshape(-1)
+        if pooling == "head_dim":
+            return s.repeat(self.n_vh), s
+        return s, s
+
+
+@dataclasses.dataclass
+class Edit:
+    """What the fold does to one tensor: input columns times `cols`, output rows divided by `rows`, and for a norm
+    weight division by `norm` (zero_centred: of 1 + w, minus 1 after)."""
+    cols: torch.Tensor = None
+    rows: torch.Tensor = None
+    norm: torch.Tensor = None
+    zero_centred: bool = False
+
+    def apply(self, t, device):
+        w = t.to(device, torch.float32)
+        if self.cols is not None:
+            w = w * self.cols.to(device)[None, :]
+        if self.rows is not None:
+            w = w / self.rows.to(device)[:, None]
+        if self.norm is not None:
+            s = self.norm.to(device)
+            w = (1 + w) / s - 1 if self.zero_centred else w / s
+        return w
+
+
+class Smoothing:
+    """The SmoothQuant fold of one model: {tensor name: Edit}."""
+
+    def __init__(self, edits=None):
+        self.edits = dict(edits or {})
+
+    @staticmethod
+    def consumers(stats):
+        """Names of the weights whose per-input-channel maxima the plan needs."""
+        return {prefix + c for prefix, g in _groups_in(stats) for c in g.consumers}
+
+    @classmethod
+    def plan(cls, stats, weight_colmax, text_config, alpha):
+        """stats: {module: input maxima}; weight_colmax: {consumer weight name: max |W| per input channel} (absent
+        consumers are skipped); text_config: the model's head geometry."""
+        heads = _Heads(text_config)
+        edits = {}
+
+        def edit(name):
+            return edits.setdefault(name, Edit())
+
+        for prefix, g in _groups_in(stats):
+            present = [prefix + c for c in g.consumers if prefix + c in weight_colmax]
+            if not present:
+                continue
+            w = torch.stack([weight_colmax[c] for c in present]).amax(dim=0)
+            s = smoothing_factors(heads.pool(stats[prefix + g.module].float(), g.pooling), heads.pool(w, g.pooling),
+                                  alpha)
+            s_cols, s_prod = heads.spread(s, g.pooling)
+            for c in present:
+                edit(c).cols = s_cols
+            if g.fold == "rows":
+                edit(prefix + g.producer).rows = s_prod
+            else:
+                e = edit(prefix + g.producer)
+                e.norm, e.zero_centred = s_prod, g.fold == "zero_centred_norm"
+        return cls(edits)
+
+    def apply(self, name, t, device="cpu"):
+        """The smoothed float32 tensor, or None when the fold leaves `name` as it is."""
+        e = self.edits.get(name)
+        return None if e is None else e.apply(t, device)
+
+
+# ---- conversion --------------------------------------------------------------------------------------------------------
+class SourceModel:
+    """A safetensors model directory: its index, shards and config, read one shard at a time."""
+
+    def __init__(self, path):
+        self.path = path
+        self.index = json.load(open(os.path.join(path, "model.safetensors.index.json")))
+        self.shards = sorted(set(self.index["weight_map"].values()))
+        self.config = json.load(open(os.path.join(path, "config.json")))
+
+    def tensors(self, shard):
+        from safetensors import safe_open
+        with safe_open(os.path.join(self.path, shard), framework="pt") as f:
+            for name in f.keys():
+                yield name, f.get_tensor(name)
+
+    def column_maxima(self, names, device):
+        """{name: max |W| over the output rows, per input column} for the named 2-D weights present."""
+        out = {}
+        for shard in self.shards:
+            for name, t in self.tensors(shard):
+                if name in names:
+                    out[name] = t.to(device, torch.float32).abs().amax(dim=0).cpu()
+        return out
+
+    def other_files(self):
+        skip = {"model.safetensors.index.json", "config.json"}
+        for fn in sorted(os.listdir(self.path)):
+            p = os.path.join(self.path, fn)
+            if os.path.isfile(p) and not fn.startswith(".") and not fn.endswith(".safetensors") and fn not in skip:
+                yield fn, p
+
+
+@dataclasses.dataclass
+class Report:
+    quantized: int = 0
+    max_rel_err: float = 0.0
+    sum_rel_err: float = 0.0
+    bytes: int = 0
+
+    def note(self, q, scale, w):
+        e = ((q.float() * scale - w).norm() / w.norm().clamp(min=1e-12)).item()
+        self.quantized += 1
+        self.max_rel_err = max(self.max_rel_err, e)
+        self.sum_rel_err += e
+
+    def summary(self):
+        return {"quantized": self.quantized, "max_rel_err": self.max_rel_err,
+                "mean_rel_err": self.sum_rel_err / max(self.quantized, 1), "bytes": self.bytes}
+
+
+def convert_tensor(name, t, smoothing, device, report):
+    """The tensors stored for one source tensor: int8 weight + scale for a quantized linear, the smoothed float32
+    tensor for a folded one, else the tensor as stored."""
+    folded = smoothing.apply(name, t, device)
+    if QUANT_PATTERN.match(name):
+        if t.dim() != 2:
+            raise ValueError(f"{name}: a quantized linear must be 2-D, got {tuple(t.shape)}")
+        w = folded if folded is not None else t.to(device, torch.float32)
+        q, scale = quantize_per_channel(w)
+        report.note(q, scale, w)
+        return {name: q.cpu(), name + "_scale": scale.cpu()}
+    return {name: folded.cpu() if folded is not None else t}
 
 
 def convert(src, dst, device=None, calib=None, alpha=0.5, log=print):
     """Convert the bf16 safetensors model in `src` into a W8A8 int-quantized checkpoint in `dst`, one shard at a
-    time.  calib: calibration file / directory for the SmoothQuant fold (None: no smoothing).  Returns a summary."""
-    from safetensors import safe_open
+    time; calib: calibration file or directory for the SmoothQuant fold (None: no fold).  Returns a summary dict."""
     from safetensors.torch import save_file
 
-    if device is None:
-        device = "cuda" if torch.cuda.is_available() else "cpu"
-    os.makedirs(dst, exist_ok=True)
-    index = json.load(open(os.path.join(src, "model.safetensors.index.json")))
-    shards = sorted(set(index["weight_map"].values()))
-    cfg = json.load(open(os.path.join(src, "config.json")))
-    plan = ({}, {}, {})
+    device = device or ("cuda" if torch.cuda.is_available() else "cpu")
+    source = SourceModel(src)
+    smoothing = Smoothing()
     if calib is not None:
         stats = load_calibration(calib)
-        tc = cfg.get("text_config", cfg)
-        need = {c for g in smoothing_groups(stats) for c in g[1]}
-        wmax = {}
-        for shard in shards:
-            with safe_open(os.path.join(src, shard), framework="pt") as f:
-                for name in f.keys():
-                    if name in need:
-                        wmax[name] = f.get_tensor(name).to(device, torch.float32).abs().amax(dim=0).cpu()
-        plan = smoothing_plan(stats, wmax, tc, alpha)
-        log(f"smoothing (alpha {alpha}): {len(plan[0])} consumer weights")
-    new_map, total, nq, err_max = {}, 0, 0, 0.0
-    for si, shard in enumerate(shards):
-        out = {}
-        with safe_open(os.path.join(src, shard), framework="pt") as f:
-            for name in f.keys():
-                t = f.get_tensor(name)
-                ts = apply_smoothing(name, t, plan, device)
-                if QUANT_PATTERN.match(name):
-                    if t.dim() != 2:
-                        raise ValueError(f"{name}: a quantized linear must be 2-D, got {tuple(t.shape)}")
-                    w = ts if ts is not None else t.to(device, torch.float32)
-                    q, scale = quantize_per_channel(w)
-                    e = ((q.float() * scale - w).norm() / w.norm().clamp(min=1e-12)).item()
-                    err_max, nq = max(err_max, e), nq + 1
-                    out[name] = q.cpu()
-                    out[name + "_scale"] = scale.cpu()
-                elif ts is not None:
-                    out[name] = ts.cpu()
-                else:
-                    out[name] = t
-        for name, t in out.items():
-            new_map[name] = shard
-            total += t.numel() * t.element_size()
-        save_file(out, os.path.join(dst, shard), metadata={"format": "pt"})
-        log(f"[{si + 1}/{len(shards)}] {shard}: {len(out)} tensors, {nq} quantized so far, max rel err {err_max:.4f}")
-    json.dump({"metadata": {"total_size": total}, "weight_map": new_map},
-              open(os.path.join(dst, "model.safetensors.index.json"), "w"), indent=2)
-    for fn in os.listdir(src):
-        if fn.endswith(".safetensors") or fn in ("model.safetensors.index.json", "config.json") or fn.startswith("."):
-            continue
-        p = os.path.join(src, fn)
-        if os.path.isfile(p):
-            shutil.copy2(p, os.path.join(dst, fn))
-    cfg["quantization_config"] = quantization_config()
-    json.dump(cfg, open(os.path.join(dst, "config.json"), "w"), indent=2)
-    return {"quantized": nq, "max_rel_err": err_max, "bytes": total}
+        colmax = source.column_maxima(Smoothing.consumers(stats), device)
+        smoothing = Smoothing.plan(stats, colmax, source.config.get("text_config", source.config), alpha)
+        log(f"SmoothQuant fold, alpha {alpha}: {len(smoothing.edits)} tensors change")
+    os.makedirs(dst, exist_ok=True)
+    report, weight_map = Report(), {}
+    for i, shard in enumerate(source.shards):
+        stored = {}
+        for name, t in source.tensors(shard):
+            stored.update(convert_tensor(name, t, smoothing, device, report))
+        save_file(stored, os.path.join(dst, shard), metadata={"format": "pt"})
+        for name, t in stored.items():
+            weight_map[name] = shard
+            report.bytes += t.numel() * t.element_size()
+        log(f"shard {i + 1} of {len(source.shards)} ({shard}) written; {report.quantized} linears quantized, worst "
+            f"relative error {report.max_rel_err:.4f}")
+    with open(os.path.join(dst, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {"total_size": report.bytes}, "weight_map": weight_map}, f, indent=2)
+    for fn, p in source.other_files():
+        shutil.copy2(p, os.path.join(dst, fn))
+    cfg = dict(source.config, quantization_config=quantization_config())
+    with open(os.path.join(dst, "config.json"), "w") as f:
+        json.dump(cfg, f, indent=2)
+    return report.summary()
 
 
+# ---- loading -----------------------------------------------------------------------------------------------------------
 def _ignored(name, ignore):
     base = name[:-len(".weight")] if name.endswith(".weight") else name
     for pat in ignore:
@@ -284,8 +393,7 @@ def load(ckpt_dir, device="cuda", names=None):
     if not (wq["num_bits"] == 8 and wq["type"] == "int" and wq["symmetric"] and wq["strategy"] == "channel" and aq
             and aq["num_bits"] == 8 and aq["strategy"] == "token" and aq["dynamic"]):
         raise ValueError(f"{ckpt_dir}: config group is not W8A8 per-channel / per-token dynamic")
-    index = json.load(open(os.path.join(ckpt_dir, "model.safetensors.index.json")))
-    wmap = index["weight_map"]
+    wmap = json.load(open(os.path.join(ckpt_dir, "model.safetensors.index.json")))["weight_map"]
     want = set(wmap) if names is None else set(names)
     by_shard = {}
     for n in want:
@@ -299,14 +407,14 @@ def load(ckpt_dir, device="cuda", names=None):
     for n, t in raw.items():
         if n.endswith(".weight") and t.dtype == torch.int8:
             sn = n + "_scale"
-            if sn not in raw:
-                with safe_open(os.path.join(ckpt_dir, wmap[sn]), framework="pt") as f:
-                    raw_scale = f.get_tensor(sn)
+            if sn in raw:
+                scale = raw[sn]
             else:
-                raw_scale = raw[sn]
+                with safe_open(os.path.join(ckpt_dir, wmap[sn]), framework="pt") as f:
+                    scale = f.get_tensor(sn)
             if _ignored(n, qc.get("ignore", [])):
                 raise ValueError(f"{n} is int8 but matches the ignore list")
-            layers[n[:-len(".weight")]] = W8A8Linear(t.to(device), raw_scale.to(device))
+            layers[n[:-len(".weight")]] = W8A8Linear(t.to(device), scale.to(device))
         elif not n.endswith(".weight_scale"):
             rest[n] = t.to(device)
     return layers, rest
@@ -321,21 +429,16 @@ def fuse(layers):
 
 
 def main(argv):
-    args = list(argv)
-    calib, alpha = None, 0.5
-    if "--smooth" in args:
-        i = args.index("--smooth")
-        calib = args[i + 1]
-        del args[i:i + 2]
-    if "--alpha" in args:
-        i = args.index("--alpha")
-        alpha = float(args[i + 1])
-        del args[i:i + 2]
-    if len(args) < 2:
-        print(__doc__)
-        return 2
-    summary = convert(args[0], args[1], args[2] if len(args) > 2 else None, calib, alpha)
-    print(json.dumps(summary))
+    ap = argparse.ArgumentParser(prog="python -m vllm_turing_amd.checkpoint",
+                                 description="bf16 safetensors model -> compressed-tensors W8A8 int-quantized checkpoint")
+    ap.add_argument("src")
+    ap.add_argument("dst")
+    ap.add_argument("device", nargs="?", default=None, help="torch device for the conversion (default: a GPU if any)")
+    ap.add_argument("--smooth", metavar="CALIB", default=None,
+                    help="calibration file or directory of rank<r>[_m1] files: apply the SmoothQuant fold")
+    ap.add_argument("--alpha", type=float, default=0.5, help="SmoothQuant migration strength (default 0.5)")
+    a = ap.parse_args(argv)
+    print(json.dumps(convert(a.src, a.dst, a.device, a.smooth, a.alpha)))
     return 0
 
 
