@@ -599,7 +599,7 @@ GEMM_SHAPES = [(33, 256, 64), (256, 256, 5120), (300, 1000, 5136), (512, 512, 80
 GEMM_SPLIT_SHAPES = [(4096, 5120, 256), (2048, 12288, 128), (4160, 5136, 144), (4096, 24576, 144), (4160, 24592, 272)]
 
 
-@pytest.mark.parametrize("kernel", [1, 3, 4])
+@pytest.mark.parametrize("kernel", [1, 3, 4, 5])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES + GEMM_SPLIT_SHAPES)
 def test_i32_gemm_kernel(L, M, N, K, kernel):
     say(f"i32 gemm kernel {kernel} M={M} N={N} K={K}")

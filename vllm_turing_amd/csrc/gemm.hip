@@ -391,6 +391,12 @@ __device__ __forceinline__ void dma_part(__amdgpu_buffer_rsrc_t rsa, __amdgpu_bu
 }
 
 
+// One 1 KB direct-to-LDS load: each lane's 16 bytes at voff + k0 of the buffer into dst + 16 * lane (an offset past the
+// buffer's end writes zeros).  A plain device function for the reason given at dma_part.
+__device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int voff, int k0) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, voff, k0, 0, 0);
+}
+
 // WM x WN wavefronts (main configuration 2 x 4: two per SIMD, so one wavefront's LDS and barrier waits are covered by
 // the other's MFMAs).  Workgroup u of the grid computes quarter (or whole) tile u % SUB of super tile t_base + u / SUB.
 template <typename T, int EPI, int WM, int WN, int FM, int FN, int KB, int NS, int SPLIT = 0, bool LEAD = false,
@@ -537,6 +543,197 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
         store_tile_i32<FM, FN>(acc, static_cast<int*>(out), M, N, mb, nbw, lane);
     } else {
         __syncthreads();                                 // every wavefront is done reading the K stages
+        store_tile_lds<T, EPI, FM, FN, PITCH>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * WTM * PITCH, out, sa, sw,
+                                              bias, M, N, sa_rows, sw_rows, mb, nbw, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// gemm_pp_kernel: the 256 x 256 configuration with its two wavefront groups in alternating roles
+// ---------------------------------------------------------------------------------------------------------------------
+// The 8 wavefronts of gemm_kernel's main configuration (2 x 4 tiles of 128 x 64, two per SIMD) form two groups of
+// four, one wavefront of each per SIMD: group 0 computes rows 0..127 of the tile (activation half A0), group 1 rows
+// 128..255 (half A1); both use all 256 weight rows W.  Time is cut into slots separated by workgroup barriers.  In each
+// slot one group is in its compute phase (the 32 MFMAs of one K stage, operands in registers) while the other is in its
+// memory phase (all 24 operand fragments of its next stage read from LDS into registers, nothing else), so each
+// SIMD's matrix pipe is fed by one wavefront while its other wavefront reads LDS.  Group 0 reads stage j in slot 2j
+// and computes it in slot 2j + 1; group 1 reads it in slot 2j + 1 and computes it in slot 2j + 2.
+//
+// Two 64 KB stage buffers (A0 | A1 | W).  A0 of a stage is read only by group 0, A1 only by group 1, W by both, so
+// each region of stage j's buffer is released as soon as its readers are done: A0 after slot 2j, A1 and W after slot
+// 2j + 1.  The loads of stage j + 2 into that buffer are issued by the computing group, spread between its MFMAs:
+//   slot 2j + 1 (group 0): A1 of stage j + 1 and A0 of stage j + 2  (4 + 4 loads of 1 KB per wavefront),
+//   slot 2j + 2 (group 1): W of stage j + 2                          (8 loads per wavefront),
+// so every region has at least two slots to land, and before each barrier a wavefront waits (vmcnt, exact counts,
+// vector memory operations retire in order) for its own loads of the regions read in the next slot.  No group refills
+// a region from its memory phase.  Group 0 passes one extra barrier at the end so both groups pass the same number.
+template <typename T, int EPI, bool KFULL, int GM = GROUP_M, bool PRIO = true>
+__global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                      const float* __restrict__ sa, const float* __restrict__ sw,
+                                                      const uint16_t* __restrict__ bias, void* __restrict__ out,
+                                                      int M, int N, int K, int sa_rows, int sw_rows, int t_base) {
+    extern __shared__ v4i ldsx[];
+    constexpr int WM = 2, WN = 4, FM = 4, FN = 2, KB = 128, NS = 2;
+    using Cfg = GemmCfg<WM, WN, FM, FN, KB, NS>;
+    constexpr int BM = Cfg::BM, WTM = 32 * FM, WTN = 32 * FN, PITCH = WTN * 2 + 8, SUBS = KB / 32;
+    constexpr int CPR = Cfg::CPR, RPB = Cfg::RPB;        // 8 chunks of 16 bytes per staged row, 8 rows per 1 KB
+    static_assert(Cfg::SUB == 1 && WM == 2 && NS == 2 && RPB == 8, "one super tile per workgroup, two groups");
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int grp = wave / WN, gw = wave % WN;           // group, wavefront within the group (== wn)
+
+    // tile mapping of gemm_kernel (XCD-aware remap, raster groups of GM super-tile rows)
+    const int TM = (M + SUPER - 1) / SUPER, TN = (N + SUPER - 1) / SUPER;
+    const int nb = gridDim.x, per = nb >> 3;
+    int u = blockIdx.x;
+    if (u < per * 8) u = (u & 7) * per + (u >> 3);
+    const int t = t_base + u;
+    const int gsz = GM * TN, gi = t / gsz, first_m = gi * GM;
+    const int gm = min(TM - first_m, GM);
+    const int m0 = (first_m + (t % gsz) % gm) * SUPER, n0 = ((t % gsz) / gm) * SUPER;
+    if (m0 >= M || n0 >= N) return;                     // uniform over the workgroup, before any barrier
+
+    // This wavefront's 8 loads per pass: group 0 owns A blocks gw * 4 + 0..3 of each half (A1 first, then A0), group
+    // 1 owns W blocks gw * 8 + 0..7 (1 KB blocks of 8 staged rows).  Lane l of a block lands at row l / 8, chunk
+    // position l % 8 and fetches the logical chunk the swizzle stores there, which depends on the block's parity only.
+    // A load's byte offset is the block's first row times K (wave-uniform) plus a per-lane part; rows past M (or N)
+    // fall outside the buffer and read as zeros (their results are never stored).
+    const __amdgpu_buffer_rsrc_t rs = grp == 0 ? make_rsrc(a, (long)M * K) : make_rsrc(w, (long)N * K);
+    const int drow = lane / CPR, pch = lane % CPR;
+    const int ch0 = pch ^ swz<CPR>(drow), ch1 = pch ^ swz<CPR>(8 + drow);   // blocks of even / odd index
+    const unsigned lane0 = (unsigned)(drow * K + ch0 * 16), lane1 = (unsigned)(drow * K + ch1 * 16);
+    const unsigned org = (unsigned)(grp == 0 ? m0 : n0);
+    uint8_t* const lbase = reinterpret_cast<uint8_t*>(ldsx);
+    // load q of this wavefront for stage `st` into stage buffer st % 2
+    auto load = [&](int q, int st) {
+        const int blk = grp == 0 ? (q < 4 ? 16 : 0) + gw * 4 + (q & 3) : gw * 8 + q;   // block within A or W
+        const int lrow = (grp == 0 ? 0 : BM) + blk * RPB;                                 // staged row in the buffer
+        const unsigned base = (org + (unsigned)(blk * RPB)) * (unsigned)K;
+        const int k0 = st * KB;
+        unsigned voff = base + ((q & 1) ? lane1 : lane0);
+        if constexpr (!KFULL) {                          // a K chunk past the end reads as zeros
+            if (k0 + ((q & 1) ? ch1 : ch0) * 16 >= K) voff = 0x7fffffffu;
+        }
+        dma_block(rs, lbase + (st & 1) * Cfg::STAGE_BYTES + lrow * KB, (int)voff, k0);
+    };
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+    v4i fa[SUBS][FM], fw[SUBS][FN];
+    auto read_frags = [&](int st) {                     // memory phase: every fragment of stage st into registers
+        const v4i* la = reinterpret_cast<const v4i*>(lbase + (st & 1) * Cfg::STAGE_BYTES);
+        const v4i* lw = la + BM * CPR;
+#pragma unroll
+        for (int sub = 0; sub < SUBS; ++sub) {
+            const int cc = 2 * sub + (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int row = grp * WTM + i * 32 + (lane & 31);
+                fa[sub][i] = la[row * CPR + (cc ^ swz<CPR>(row))];
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int row = gw * WTN + j * 32 + (lane & 31);
+                fw[sub][j] = lw[row * CPR + (cc ^ swz<CPR>(row))];
+            }
+        }
+    };
+    // compute phase: the stage's 32 MFMAs, with loads 0..3 (stage st_a) if HA and loads 4..7 (stage st_b) if HB issued
+    // one after every 4 MFMAs (HA, HB compile-time, so no branch sits between the MFMAs)
+    auto compute = [&](auto HA, auto HB, int st_a, int st_b) {
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int sub = 0; sub < SUBS; ++sub) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int i = 2 * h; i < 2 * h + 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[sub][j], fa[sub][i], acc[i][j], 0, 0, 0);
+                const int q = sub * 2 + h;               // load q: 0..3 of pass a, 4..7 of pass b
+                __builtin_amdgcn_sched_barrier(0);
+                if (q < 4) {
+                    if constexpr (decltype(HA)::value) load(q, st_a);
+                } else {
+                    if constexpr (decltype(HB)::value) load(q, st_b);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+    };
+    using Y = std::integral_constant<bool, true>;
+    using NO = std::integral_constant<bool, false>;
+    auto slot_end = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto wait_vm = [&](int n) {                         // at most n of this wavefront's loads outstanding
+        if (n >= 8) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+        else if (n >= 4) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    };
+    constexpr int LGKM0 = 0xc07f;
+
+    const int nk = (K + KB - 1) / KB;
+    // prologue: stage 0 whole (group 0: A1 and A0, group 1: W), group 0 also A0 of stage 1, group 1 also W of stage 1
+#pragma unroll
+    for (int q = 0; q < 8; ++q) load(q, 0);
+    if (nk > 1) {
+        if (grp == 0) {
+#pragma unroll
+            for (int q = 4; q < 8; ++q) load(q, 1);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) load(q, 1);
+        }
+    }
+    wait_vm(nk > 1 ? (grp == 0 ? 4 : 8) : 0);            // stage 0 landed
+    slot_end();
+    // Each stage j: memory phase, then compute phase.  Group 0's compute phase of stage j loads A1 of stage j + 1 and
+    // A0 of stage j + 2, group 1's loads W of stage j + 2, where those stages exist; the last two stages are peeled so
+    // that which loads exist is known at compile time.
+    if (grp == 0) {
+        auto stage = [&](int j, auto HA, auto HB) {
+            read_frags(j);                              // slot 2j: memory phase
+            __builtin_amdgcn_s_waitcnt(LGKM0);
+            wait_vm(j + 1 < nk ? 4 : 0);                // A1 of stage j landed (A0 of stage j + 1 may be in flight)
+            slot_end();
+            compute(HA, HB, j + 1, j + 2);              // slot 2j + 1: MFMAs, A1 of j + 1, A0 of j + 2
+            wait_vm(4 * decltype(HA)::value + 4 * decltype(HB)::value);   // A0 of stage j + 1 landed
+            slot_end();
+        };
+        int j = 0;
+        for (; j + 2 < nk; ++j) stage(j, Y{}, Y{});
+        if (j + 1 < nk) stage(j++, Y{}, NO{});
+        stage(j, NO{}, NO{});
+        slot_end();                                     // slot 2 nk: group 1 computes the last stage
+    } else {
+        auto stage = [&](int j, auto HW) {
+            read_frags(j);                              // slot 2j + 1: memory phase
+            __builtin_amdgcn_s_waitcnt(LGKM0);
+            wait_vm(0);                                 // W of stage j + 1 landed
+            slot_end();
+            compute(HW, HW, j + 2, j + 2);              // slot 2j + 2: MFMAs, W of stage j + 2
+            slot_end();
+        };
+        slot_end();                                     // slot 0: group 0 reads stage 0
+        int j = 0;
+        for (; j + 2 < nk; ++j) stage(j, Y{});
+        for (; j < nk; ++j) stage(j, NO{});
+    }
+
+    const int mb = m0 + grp * WTM, nbw = n0 + gw * WTN;
+    if constexpr (EPI == EPI_I32) {
+        store_tile_i32<FM, FN>(acc, static_cast<int*>(out), M, N, mb, nbw, lane);
+    } else {
+        __syncthreads();
         store_tile_lds<T, EPI, FM, FN, PITCH>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * WTM * PITCH, out, sa, sw,
                                               bias, M, N, sa_rows, sw_rows, mb, nbw, lane);
     }
@@ -1194,6 +1391,30 @@ constexpr int LONG_ROUNDS = 6;
 #define W8_SMALL_REM_DIV 2
 #endif
 
+#ifndef W8_GEMM_PP
+#define W8_GEMM_PP 1
+#endif
+// The main configuration with its wavefront groups in alternating roles (gemm_pp_kernel).
+template <typename T, int EPI>
+static void launch_gemm_pp(const Args& p, int t_base, int blocks) {
+    using G = GemmCfg<MainCfg::WM, MainCfg::WN, MainCfg::FM, MainCfg::FN, MainCfg::KB, MainCfg::NS>;
+    if (p.K % MainCfg::KB == 0) {
+        const void* kern = reinterpret_cast<const void*>(&gemm_pp_kernel<T, EPI, true>);
+        static const hipError_t attr =
+            hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+        (void)attr;
+        gemm_pp_kernel<T, EPI, true><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
+            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
+    } else {
+        const void* kern = reinterpret_cast<const void*>(&gemm_pp_kernel<T, EPI, false>);
+        static const hipError_t attr =
+            hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+        (void)attr;
+        gemm_pp_kernel<T, EPI, false><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
+            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
+    }
+}
+
 template <typename T, int EPI, typename C>
 static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
     using G = GemmCfg<C::WM, C::WN, C::FM, C::FN, C::KB, C::NS>;
@@ -1257,12 +1478,15 @@ static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
     const int cus = cu_count();
     const int full = tiles / cus * cus, rem = tiles - full;
     const bool longk = tiles >= LONG_ROUNDS * cus;
-    if (policy == 0 || rem == 0 || rem > cus / W8_SMALL_REM_DIV) {
-        if (longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, tiles);
+    const bool pp = policy == 3 || (W8_GEMM_PP && policy != 0);
+    if (policy == 0 || policy == 3 || rem == 0 || rem > cus / W8_SMALL_REM_DIV) {
+        if (pp) launch_gemm_pp<T, EPI>(p, 0, tiles);
+        else if (longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, tiles);
         else launch_gemm_cfg<T, EPI, MainCfg>(p, 0, tiles);
         return;
     }
-    if (full > 0 && longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, full);
+    if (full > 0 && pp) launch_gemm_pp<T, EPI>(p, 0, full);
+    else if (full > 0 && longk) launch_gemm_cfg<T, EPI, LongCfg>(p, 0, full);
     else if (full > 0) launch_gemm_cfg<T, EPI, MainCfg>(p, 0, full);
     // the remainder as quarter tiles: with 4 K stages where they fit in one round at one workgroup per CU, else with 2
     // (two workgroups per CU)
@@ -1351,7 +1575,7 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 // M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120; kernel 3 = the prefill kernel's quarter-tile configuration alone;
 // kernel 4 = its full-tile configuration alone).  Returns -1 on bad arguments, else the launch error.
 extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream) {
-    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 4) return -1;
+    if (check_common(a, w, M, N, K, DT_F16) != 0 || kernel < 0 || kernel > 5) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, nullptr, nullptr, nullptr, acc, M, N, K, 0, 0,
                  (hipStream_t)stream};
     if (kernel == 0) {
@@ -1365,6 +1589,8 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
         launch_gemm<f16, EPI_I32>(p, 2);
     } else if (kernel == 4) {
         launch_gemm<f16, EPI_I32>(p, 0);
+    } else if (kernel == 5) {
+        launch_gemm<f16, EPI_I32>(p, 3);
     } else {
         if (!dot4_ok(p)) return -1;
         launch_dot4<f16, EPI_I32>(p);
