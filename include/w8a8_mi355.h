@@ -109,8 +109,9 @@ int w8a16_mma(const void* x, const void* w, const void* s, const void* bias, voi
 /* Test export: the raw int32 accumulators acc [M, N] = a . w^T of one kernel's main loop, for bit-exact accumulator
  * checks: kernel 0 the small-M MFMA streaming kernel (M <= 64), 1 the prefill kernel as dispatched, 2 the v_dot4
  * streaming kernel (M = 1 and K <= 17408, M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120), 3 and 4 the prefill
- * kernel's quarter-tile and full-tile configurations alone.  No counterpart in the reference.  Returns -1 on bad
- * arguments, else the HIP launch error. */
+ * kernel's quarter-tile and full-tile (single-role wavefronts) configurations alone, 5 the full-tile configuration
+ * with alternating wavefront groups alone.  No counterpart in the reference.  Returns -1 on bad arguments, else the
+ * HIP launch error. */
 int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, int K, int kernel, void* stream);
 
 /* Test export: silu_mul_quant (dtype 0) / silu_mul_quant_bf16 (dtype 1) through one of its two kernels, path 1 the

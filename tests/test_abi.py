@@ -62,7 +62,7 @@ def test_argument_validation_codes(L):
     assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # K <= 17408 at one row
     assert L.w8a8_i32(16, 16, 0, 2, 64, 8208, 2, None) == -1                     # K <= 8192 at two rows
     assert L.w8a8_i32(16, 16, 0, 4, 64, 5136, 2, None) == -1                     # K <= 5120 at four rows
-    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 5, None) == -1
+    assert L.w8a8_i32(16, 16, 0, 4, 64, 64, 6, None) == -1
     assert L.w8a8_i32(16, 16, 0, 40, 64, 131072, 1, None) == -1                 # K < 131072: exact int32 sums
     assert L.w8a8_scaled_mm(16, 16, 0, 0, None, 0, 40, 64, 131072, 1, 1, 0, None) == -1
     # silu_mul_quant: 1 = bad I, 0 for M == 0 (csrc/silu_quant.cu:72-73)
