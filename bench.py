@@ -332,7 +332,8 @@ def bench_stack(torch, L, st, dev, ms_list=(1, 4, 4096)):
     H, I = workloads.HIDDEN, workloads.INTERMEDIATE
     res = {"workload": f"64-layer linear stack, {len(shapes)} projections, {n_params / 1e9:.2f} G int8 weights, "
                        f"bf16 activations; per layer residual add + RMSNorm + quant -> mixer in -> quant -> mixer out "
-                       f"-> residual add + RMSNorm + quant -> gate_up -> SiLU*up+quant -> down", "passes": {}}
+                       f"-> residual add + RMSNorm + quant -> gate_up -> SiLU*up+quant -> down; at M <= 12 the mixer "
+                       f"out-projection quantizes its input inside the GEMV (w8a8_gemv_quant)", "passes": {}}
     for M in ms_list:
         kmax = max(K for (_, _, _, K) in shapes)
         nmax = max(N for (_, _, N, _) in shapes)
@@ -359,6 +360,11 @@ def bench_stack(torch, L, st, dev, ms_list=(1, 4, 4096)):
                         raise RuntimeError("rms_norm_quant")
                     dst = o
                 else:                                             # mixer out: the mixer core's output
+                    if M <= 12:                                   # quantization fused into the decode GEMV
+                        if L.w8a8_gemv_quant(y.data_ptr(), K, q.data_ptr(), s.data_ptr(), w.data_ptr(), sw.data_ptr(),
+                                             None, o.data_ptr(), M, N, K, 1, 1, st()) != 0:
+                            raise RuntimeError("w8a8_gemv_quant")
+                        continue
                     if L.per_token_quant(y.data_ptr(), q.data_ptr(), s.data_ptr(), M, K, K, 1, st()) != 0:
                         raise RuntimeError("per_token_quant")
                     dst = o

@@ -28,6 +28,17 @@ int w8a8_gemv(const void* a, const void* w, const void* sa, const void* sw, cons
 int w8a8_mma(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out, int M, int N,
              int K, int sa_rows, int sw_rows, int dtype, void* stream);
 
+/* The small-M W8A8 GEMV from 16-bit activations, quantization fused: x [M, K] fp16 (dtype 0) / bf16 (dtype 1) with
+ * row stride ldx elements is quantized per token exactly as per_token_quant does (its int8 rows and float32 scales are
+ * written to xq [M, K] and xs [M]) and multiplied as w8a8_gemv does (small-M epilogue, sa = xs), M in [1, 16]; out
+ * [M, N] in the same dtype.  At one row (K <= 17408, x 16-byte aligned, ldx % 8 == 0) each workgroup quantizes the
+ * row itself, so no separate quantization launch runs (the decode o_proj / out_proj input); otherwise the two steps
+ * run as two launches.  No counterpart in the reference, whose
+ * quantization is fused into the producer by inductor (vllm_turing/quantfuse.py:1-10).  Returns -1 on bad arguments,
+ * else the HIP launch error. */
+int w8a8_gemv_quant(const void* x, long ldx, void* xq, void* xs, const void* w, const void* sw, const void* bias,
+                    void* out, int M, int N, int K, int sw_rows, int dtype, void* stream);
+
 /* Prefill W8A8 GEMM, any M (dispatched for M > 32), per-row sa [M] and per-column sw [N], no bias, N % 16 == 0:
  * out[m, n] = T(sa[m] * float(float(acc) * sw[n])).
  * Replaces vllm_turing/csrc/w8a8_big.cu:66 (same arguments).  Returns 0 ok, 1 cannot implement (shape, alignment),

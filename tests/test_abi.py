@@ -94,6 +94,11 @@ def test_argument_validation_codes(L):
     assert L.w8a16_mma(16, 16, 16, None, 16, 33, 64, 5120, 2, None) == -2
     assert L.w8a16_mma(8, 16, 16, None, 16, 8, 64, 512, 2, None) == -1             # x 16-byte aligned
     assert L.w8a16_mma(None, 16, 16, None, 16, 8, 64, 512, 2, None) == -1
+    assert L.w8a8_gemv_quant(16, 64, 16, 16, 16, 16, None, 16, 17, 64, 64, 1, 0, None) == -1     # M <= 16
+    assert L.w8a8_gemv_quant(16, 32, 16, 16, 16, 16, None, 16, 4, 64, 64, 1, 0, None) == -1      # ldx >= K
+    assert L.w8a8_gemv_quant(None, 64, 16, 16, 16, 16, None, 16, 4, 64, 64, 1, 0, None) == -1    # x
+    assert L.w8a8_gemv_quant(16, 64, 16, 16, 16, 16, None, 16, 4, 64, 72, 1, 0, None) == -1      # K % 16
+    assert L.w8a8_gemv_quant(16, 64, 8, 16, 16, 16, None, 16, 4, 64, 64, 1, 0, None) == -1       # xq aligned
     assert L.hbm_read(None, 1024, 16, None) == -1
     assert L.hbm_read(16, 1000, 16, None) == -1                                    # bytes % 16
     assert L.hbm_read(8, 1024, 16, None) == -1                                     # 16-byte aligned

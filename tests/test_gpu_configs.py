@@ -131,14 +131,15 @@ def test_stack_shapes(L, M):
 
 def test_stack_pass_m4(L):
     """One whole pass of the 64-layer stack at M = 4 (24.33 G int8 weights, random per layer), every layer as the
-    stack benchmark runs it: residual add + RMSNorm + quant -> mixer in-projection -> quant of the mixer output ->
-    out-projection -> residual add + RMSNorm + quant -> gate_up -> SiLU*up + quant -> down.  The mixer core is not on
+    stack benchmark runs it: residual add + RMSNorm + quant -> mixer in-projection -> out-projection of the mixer
+    output with its quantization fused into the GEMV (w8a8_gemv_quant) -> residual add + RMSNorm + quant -> gate_up ->
+    SiLU*up + quant -> down.  The mixer core is not on
     the path: its output is stood in for by the first 6144 columns of the in-projection (a strided view, so the
     per-token quant reads rows with a stride), which keeps every layer dependent on the previous one.  The final
     hidden state and residual stream are compared bit for bit with the same pass on the CPU."""
     say("stack pass M=4, 64 layers")
-    from vllm_turing_amd import (workloads, rms_norm_dynamic_per_token_quant, cutlass_scaled_mm, per_token_quant,
-                                 silu_mul_quant)
+    from vllm_turing_amd import workloads, rms_norm_dynamic_per_token_quant, cutlass_scaled_mm, silu_mul_quant
+    from vllm_turing_amd.w8a8 import gemv_quant
     M, H, I = 4, workloads.HIDDEN, workloads.INTERMEDIATE
     shapes = workloads.stack_shapes()
     gdev = torch.Generator(device=DEV).manual_seed(7)
@@ -160,8 +161,7 @@ def test_stack_pass_m4(L):
         (w_in, s_in), (w_out, s_out), (w_gu, s_gu), (w_dn, s_dn) = weights[4 * li:4 * li + 4]
         q, s = rms_norm_dynamic_per_token_quant(h, norms_d[2 * li], 1e-6, torch.int8, None, r)
         y = cutlass_scaled_mm(q, w_in.t(), s, s_in, torch.bfloat16)
-        q, s = per_token_quant(y[:, :core])
-        h = cutlass_scaled_mm(q, w_out.t(), s, s_out, torch.bfloat16)
+        h = gemv_quant(y[:, :core], w_out, s_out)       # quantization inside the decode GEMV (strided rows)
         q, s = rms_norm_dynamic_per_token_quant(h, norms_d[2 * li + 1], 1e-6, torch.int8, None, r)
         gu = cutlass_scaled_mm(q, w_gu.t(), s, s_gu, torch.bfloat16)
         q, s = silu_mul_quant(gu)

@@ -701,6 +701,65 @@ def test_scaled_mm_bits(L, M, N, K, dt, with_bias, per_tensor, order):
     assert not over.any(), f"{int(over.sum())} outputs further than one 16-bit ulp from the exact value"
 
 
+GEMV_QUANT_CASES = [
+    # M, N, K, dtype, ldx extra, bias, zero row
+    (1, 5120, 6144, torch.bfloat16, 0, False, False),     # out_proj / o_proj at M = 1
+    (4, 5120, 6144, torch.bfloat16, 0, False, True),      # M = 4 at K = 6144: the fallback (quant kernel + GEMV)
+    (2, 5120, 6144, torch.float16, 64, True, True),       # strided rows, bias, a zero row
+    (3, 1000, 8192, torch.bfloat16, 8, True, False),
+    (1, 5120, 17408, torch.float16, 0, False, False),     # the longest K of the fused kernel at one row
+    (5, 333, 5120, torch.float16, 0, True, True),
+    (1, 96, 272, torch.bfloat16, 0, False, False),        # K not a multiple of the 1 KB row chunk
+    (8, 4096, 5120, torch.bfloat16, 0, False, True),      # M = 8: fallback
+    (12, 2048, 1024, torch.float16, 16, True, False),
+]
+
+
+@pytest.mark.parametrize("M,N,K,dt,extra,with_bias,zero_row", GEMV_QUANT_CASES)
+def test_gemv_quant_bits(L, M, N, K, dt, extra, with_bias, zero_row):
+    """w8a8_gemv_quant (quantization fused into the GEMV) against per_token_quant + w8a8_gemv and the oracle: the
+    int8 rows, scales and outputs bit for bit."""
+    say(f"gemv_quant M={M} N={N} K={K} {dt} ldx+{extra} bias={with_bias}")
+    from vllm_turing_amd import w8a8
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    xf = torch.randn(M, K + extra, generator=g)
+    xf[:, torch.randperm(K, generator=g)[:max(1, K // 200)]] *= 20
+    if zero_row:
+        xf[M // 2] = 0
+    xfull = xf.to(dt)
+    x = xfull[:, :K]                                              # rows of stride K + extra
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, generator=g)
+    sw = torch.rand(N, 1, generator=g) * 1e-2 + 1e-4
+    bias = torch.randn(N, generator=g).to(dt) if with_bias else None
+    xd = xfull.to(DEV)[:, :K]
+    wd, swd, bd = w.to(DEV), sw.to(DEV), (bias.to(DEV) if bias is not None else None)
+    out = torch.empty(M, N, dtype=dt, device=DEV)
+    xq = torch.empty(M, K, dtype=torch.int8, device=DEV)
+    xs = torch.empty(M, dtype=torch.float32, device=DEV)
+    assert L.w8a8_gemv_quant(xd.data_ptr(), xd.stride(0), xq.data_ptr(), xs.data_ptr(), wd.data_ptr(), swd.data_ptr(),
+                             bd.data_ptr() if bd is not None else None, out.data_ptr(), M, N, K, 1, code(dt),
+                             stream()) == 0
+    # the two-launch route
+    q2 = torch.empty(M, K, dtype=torch.int8, device=DEV)
+    s2 = torch.empty(M, dtype=torch.float32, device=DEV)
+    out2 = torch.empty(M, N, dtype=dt, device=DEV)
+    assert L.per_token_quant(xd.data_ptr(), q2.data_ptr(), s2.data_ptr(), M, K, xd.stride(0), code(dt), stream()) == 0
+    assert L.w8a8_gemv(q2.data_ptr(), wd.data_ptr(), s2.data_ptr(), swd.data_ptr(),
+                       bd.data_ptr() if bd is not None else None, out2.data_ptr(), M, N, K, 1, 1, code(dt),
+                       stream()) == 0
+    y = w8a8.gemv_quant(xd, wd, swd, bd) if w8a8.gemv_quant_ok(xd, wd, swd, bd) else None
+    torch.cuda.synchronize()
+    assert torch.equal(xq, q2) and torch.equal(xs.view(torch.int32), s2.view(torch.int32))
+    assert torch.equal(out, out2)
+    qr, sr = oracle.quant_rows(x.contiguous())
+    assert np.array_equal(xq.cpu().numpy(), qr) and np.array_equal(xs.cpu().numpy(), sr)
+    ref = oracle.epilogue(oracle.gemm_i32(qr, w.numpy()), sr, sw.numpy(), None if bias is None else bits(bias),
+                          code(dt), oracle.ORDER_SMALL_M)
+    assert np.array_equal(bits(out), ref)
+    if y is not None:
+        assert torch.equal(y, out)
+
+
 def test_dispatch_paths(L):
     from vllm_turing_amd import w8a8
     K, N = 5120, 1024

@@ -101,27 +101,26 @@ __device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sa
 // registers for the whole kernel.  Rows are grid-strided over the wavefronts, R rows per iteration with the next
 // iteration's loads issued before this one's v_dot4 math (double buffering).  Each row's per-lane partial sums are
 // reduced across the wavefront with DPP row operations, ds_swizzle and readlane.
-template <typename T, int M, int CH, int R, int EPI, bool NT = true>
+// QX: the activations arrive as fp16 / bf16 rows x (row stride ldx elements, the output type) and every workgroup
+// quantizes them into LDS before its first row's math, with per_token_quant's arithmetic (absmax over the row; scale
+// = absmax / 127; q = clamp(rint(x * (127 / absmax)))), while its wavefronts' first weight rows are already being
+// loaded (each workgroup reads the row once: per wavefront it cost ~140 MB of L2 reads at N = 5120); workgroup 0 also
+// writes the int8 rows to xq and the scales to xs.
+template <typename T, int M, int CH, int R, int EPI, bool NT = true, bool QX = false>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
                                                         const uint16_t* __restrict__ bias, void* __restrict__ out,
-                                                        int N, int K, int sa_rows, int sw_rows) {
+                                                        int N, int K, int sa_rows, int sw_rows,
+                                                        const uint16_t* __restrict__ x = nullptr, long ldx = 0,
+                                                        int8_t* __restrict__ xq = nullptr,
+                                                        float* __restrict__ xs = nullptr) {
     const int lane = threadIdx.x & 63;
     const int nw = gridDim.x * (blockDim.x >> 6);
     const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int K16 = K >> 4;
     const v4i z = {0, 0, 0, 0};
     v4i av[M][CH];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int c = lane + 64 * j;
-            av[m][j] = c < K16 ? *reinterpret_cast<const v4i*>(a + (long)m * K + c * 16) : z;
-        }
     float sam[M];                                        // row scales (none are read for the int32 output)
-#pragma unroll
-    for (int m = 0; m < M; ++m) sam[m] = EPI == EPI_I32 ? 0.0f : sa[sa_rows ? m : 0];
     v4i wb[2][R][CH];
     float swb[2][R];                                     // the rows' column scale and bias bits, loaded with the row
     uint16_t bb[2][R];
@@ -174,9 +173,77 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
     // loop is peeled so that no load sits under a condition: then the compiler's wait before a group's math counts
     // the next group's loads as still outstanding instead of waiting for them too.
     const int stride = R * nw;
-    if (wid >= N) return;
-    const int cnt = (N - 1 - wid) / stride + 1;
-    load(0, wid);
+    if constexpr (!QX) {
+        if (wid >= N) return;
+    }
+    const int cnt = wid < N ? (N - 1 - wid) / stride + 1 : 0;
+    load(0, wid);                                        // rows past N read row N - 1 (see load)
+    if constexpr (QX) {
+        // The workgroup quantizes the rows once into LDS (xl: M rows of K int8), each thread 8 values per step:
+        // absmax over the row (wavefront max, then across the wavefronts), then the int8 values from a second read
+        // of the same (now cached) row; the wavefronts then take their chunks from LDS.  Workgroup 0 also writes
+        // the int8 rows and scales out.
+        extern __shared__ v4i xq_lds[];
+        int8_t* xl = reinterpret_cast<int8_t*>(xq_lds);
+        float* red = reinterpret_cast<float*>(xl + M * K);   // one float per wavefront
+        const int nthr = blockDim.x, tid = threadIdx.x, nvec = K >> 3;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const uint4* xr = reinterpret_cast<const uint4*>(x + m * ldx);
+            float amax = 0.0f;
+            for (int v = tid; v < nvec; v += nthr) {
+                const uint4 u = xr[v];
+                const uint32_t e4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    amax = __builtin_fmaxf(amax, __builtin_fabsf(lo_half(e4[e], T{})));
+                    amax = __builtin_fmaxf(amax, __builtin_fabsf(hi_half(e4[e], T{})));
+                }
+            }
+            amax = wave_max(amax);
+            if (nthr > 64) {
+                if (lane == 0) red[threadIdx.x >> 6] = amax;
+                __syncthreads();
+                for (int i = 0; i < (nthr >> 6); ++i) amax = __builtin_fmaxf(amax, red[i]);
+                __syncthreads();                         // red is reused by the next row
+            }
+            const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+            sam[m] = amax / 127.0f;
+            if (blockIdx.x == 0 && tid == 0) xs[m] = sam[m];
+            for (int v = tid; v < nvec; v += nthr) {
+                const uint4 u = xr[v];
+                const uint32_t e4[4] = {u.x, u.y, u.z, u.w};
+                int b[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    b[2 * e] = q8(lo_half(e4[e], T{}) * inv);
+                    b[2 * e + 1] = q8(hi_half(e4[e], T{}) * inv);
+                }
+                const uint2 q2 = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
+                *reinterpret_cast<uint2*>(xl + m * K + v * 8) = q2;
+                if (blockIdx.x == 0) *reinterpret_cast<uint2*>(xq + (long)m * K + v * 8) = q2;
+            }
+        }
+        __syncthreads();
+        if (wid >= N) return;                            // after the workgroup's barriers: no rows of its own
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int c = lane + 64 * j;
+                av[m][j] = c < K16 ? *reinterpret_cast<const v4i*>(xl + m * K + c * 16) : z;
+            }
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int c = lane + 64 * j;
+                av[m][j] = c < K16 ? *reinterpret_cast<const v4i*>(a + (long)m * K + c * 16) : z;
+            }
+#pragma unroll
+        for (int m = 0; m < M; ++m) sam[m] = EPI == EPI_I32 ? 0.0f : sa[sa_rows ? m : 0];
+    }
     int k = 0;
     for (; k + 2 < cnt; k += 2) {
         load(1, wid + (k + 1) * stride);
@@ -566,7 +633,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 //   slot 2j + 2 (group 1): W of stage j + 2                          (8 loads per wavefront),
 // so every region has at least two slots to land, and before each barrier a wavefront waits (vmcnt, exact counts,
 // vector memory operations retire in order) for its own loads of the regions read in the next slot.  No group refills
-// a region from its memory phase.  Group 0 passes one extra barrier at the end so both groups pass the same number.
+// a region from its memory phase.  Group 0 begins its epilogue while group 1 computes the last stage.
 template <typename T, int EPI, bool KFULL, int GM = GROUP_M, bool PRIO = true>
 __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                       const float* __restrict__ sa, const float* __restrict__ sw,
@@ -713,27 +780,29 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__
         for (; j + 2 < nk; ++j) stage(j, Y{}, Y{});
         if (j + 1 < nk) stage(j++, Y{}, NO{});
         stage(j, NO{}, NO{});
-        slot_end();                                     // slot 2 nk: group 1 computes the last stage
     } else {
-        auto stage = [&](int j, auto HW) {
+        auto stage = [&](int j, auto HW, auto LAST) {
             read_frags(j);                              // slot 2j + 1: memory phase
             __builtin_amdgcn_s_waitcnt(LGKM0);
             wait_vm(0);                                 // W of stage j + 1 landed
             slot_end();
             compute(HW, HW, j + 2, j + 2);              // slot 2j + 2: MFMAs, W of stage j + 2
-            slot_end();
+            if constexpr (!decltype(LAST)::value) slot_end();
         };
         slot_end();                                     // slot 0: group 0 reads stage 0
         int j = 0;
-        for (; j + 2 < nk; ++j) stage(j, Y{});
-        for (; j < nk; ++j) stage(j, NO{});
+        for (; j + 2 < nk; ++j) stage(j, Y{}, NO{});
+        if (j + 1 < nk) stage(j++, NO{}, NO{});
+        stage(j, NO{}, Y{});
     }
+    // Epilogue: group 0 starts while group 1 computes the last stage (slot 2 nk).  Every load has landed and the last
+    // reads of the stage buffers ended before the barrier closing slot 2 nk - 1, and each wavefront transposes through
+    // its own LDS region, so no further barrier is needed (both groups passed 2 nk + 1).
 
     const int mb = m0 + grp * WTM, nbw = n0 + gw * WTN;
     if constexpr (EPI == EPI_I32) {
         store_tile_i32<FM, FN>(acc, static_cast<int*>(out), M, N, mb, nbw, lane);
     } else {
-        __syncthreads();
         store_tile_lds<T, EPI, FM, FN, PITCH>(acc, reinterpret_cast<uint8_t*>(ldsx) + wave * WTM * PITCH, out, sa, sw,
                                               bias, M, N, sa_rows, sw_rows, mb, nbw, lane);
     }
@@ -1169,6 +1238,11 @@ struct Args {
     void* out;
     int M, N, K, sa_rows, sw_rows;
     hipStream_t st;
+    // the VALU GEMV with in-kernel activation quantization: 16-bit rows x (stride ldx), int8 copy xq, scales xs
+    const uint16_t* x = nullptr;
+    long ldx = 0;
+    int8_t* xq = nullptr;
+    float* xs = nullptr;
 };
 
 // One to five activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
@@ -1205,27 +1279,43 @@ static int row_stream_per_cu(const void* kern) {
     return nb < DOT4_BLOCKS_PER_CU ? nb : DOT4_BLOCKS_PER_CU;
 }
 
-template <typename T, int M, int CH, int EPI>
+template <typename T, int M, int CH, int EPI, bool QX = false>
 static void launch_dot4_ch(const Args& p) {
     if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2) && (M < 4 || CH <= DOT4_MAX_CH_M4)) {
-        if constexpr (M <= 2) {
-            const int waves = (p.N + DOT4_ROWS_PER_WAVE - 1) / DOT4_ROWS_PER_WAVE;
-            gemv_dot4_kernel<T, M, CH, 1, EPI><<<waves, 64, 0, p.st>>>(
-                p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
+        using K_ = decltype(&gemv_dot4_kernel<T, M, CH, 1, EPI, true, QX>);
+        const K_ kern = &gemv_dot4_kernel<T, M, CH, 1, EPI, true, QX>;
+        if constexpr (QX) {                              // 4-wavefront workgroups sharing the quantized rows in LDS
+            const int lds = M * CH * 1024 + 64;          // rows of up to CH * 1024 int8, then the reduction floats
+            static const int per_cu = [&] {
+                int nb = 0;
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), 256, lds) !=
+                        hipSuccess || nb < 1)
+                    nb = 1;
+                return nb < DOT4_BLOCKS_PER_CU ? nb : DOT4_BLOCKS_PER_CU;
+            }();
+            const int need = (p.N + 3) / 4, grid = cu_count() * per_cu;
+            kern<<<need < grid ? need : grid, 256, p.M * p.K + 64, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N,
+                                                                          p.K, p.sa_rows, p.sw_rows, p.x, p.ldx,
+                                                                          p.xq, p.xs);
             return;
         }
-        static const int per_cu =
-            row_stream_per_cu(reinterpret_cast<const void*>(&gemv_dot4_kernel<T, M, CH, 1, EPI>));
+        if constexpr (M <= 2) {
+            const int waves = (p.N + DOT4_ROWS_PER_WAVE - 1) / DOT4_ROWS_PER_WAVE;
+            kern<<<waves, 64, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows, p.x,
+                                         p.ldx, p.xq, p.xs);
+            return;
+        }
+        static const int per_cu = row_stream_per_cu(reinterpret_cast<const void*>(kern));
         const int need = (p.N + 3) / 4, grid = cu_count() * per_cu;
-        gemv_dot4_kernel<T, M, CH, 1, EPI><<<need < grid ? need : grid, 256, 0, p.st>>>(
-            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows);
+        kern<<<need < grid ? need : grid, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows,
+                                                          p.sw_rows, p.x, p.ldx, p.xq, p.xs);
     }
 }
-template <typename T, int M, int EPI>
+template <typename T, int M, int EPI, bool QX = false>
 static void launch_dot4_m(const Args& p) {
     if constexpr (M <= DOT4_MAX_M) {
         switch (dot4_chunks(p.K)) {
-#define W8_CASE(C) case C: launch_dot4_ch<T, M, C, EPI>(p); break;
+#define W8_CASE(C) case C: launch_dot4_ch<T, M, C, EPI, QX>(p); break;
             W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8) W8_CASE(10)
             W8_CASE(12) W8_CASE(14) W8_CASE(17)
 #undef W8_CASE
@@ -1237,14 +1327,14 @@ static bool dot4_ok(const Args& p) {
            dot4_chunks(p.K) <= (p.M < 2 ? DOT4_MAX_CH : p.M < 4 ? DOT4_MAX_CH_M2 : DOT4_MAX_CH_M4);
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool QX = false>
 static void launch_dot4(const Args& p) {
     switch (p.M) {
-        case 1: launch_dot4_m<T, 1, EPI>(p); break;
-        case 2: launch_dot4_m<T, 2, EPI>(p); break;
-        case 3: launch_dot4_m<T, 3, EPI>(p); break;
-        case 4: launch_dot4_m<T, 4, EPI>(p); break;
-        case 5: launch_dot4_m<T, 5, EPI>(p); break;
+        case 1: launch_dot4_m<T, 1, EPI, QX>(p); break;
+        case 2: launch_dot4_m<T, 2, EPI, QX>(p); break;
+        case 3: launch_dot4_m<T, 3, EPI, QX>(p); break;
+        case 4: launch_dot4_m<T, 4, EPI, QX>(p); break;
+        case 5: launch_dot4_m<T, 5, EPI, QX>(p); break;
     }
 }
 
@@ -1536,6 +1626,35 @@ extern "C" int w8a8_mma(const void* a, const void* w, const void* sa, const void
     if (M > 32 || check_common(a, w, M, N, K, dtype) != 0) return -1;
     const Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, out,
                  M, N, K, sa_rows, sw_rows, (hipStream_t)stream};
+    dispatch_dtype_stream<EPI_SMALL>(p, dtype);
+    return (int)hipGetLastError();
+}
+
+// w8a8_gemv from 16-bit activations: x [M, K] fp16 / bf16 (dtype, also the output type; row stride ldx elements) is
+// quantized per token (per_token_quant's arithmetic) and multiplied with the small-M epilogue; the int8 rows and
+// their scales are also written to xq [M, K] and xs [M].  At one row within the VALU GEMV's K limit (x 16-byte
+// aligned, ldx % 8 == 0) each workgroup quantizes the row itself, otherwise per_token_quant runs first.
+// No counterpart in the reference (whose quantization is fused into the producer by inductor, quantfuse.py:1-10).
+extern "C" int w8a8_gemv_quant(const void* x, long ldx, void* xq, void* xs, const void* w, const void* sw,
+                               const void* bias, void* out, int M, int N, int K, int sw_rows, int dtype,
+                               void* stream) {
+    if (M > 16 || !x || !xq || !xs || ldx < K || check_common(xq, w, M, N, K, dtype) != 0) return -1;
+    Args p{(const int8_t*)xq, (const int8_t*)w, (const float*)xs, (const float*)sw, (const uint16_t*)bias, out, M, N,
+           K, 1, sw_rows, (hipStream_t)stream};
+    // one row only: at two rows the 4-wavefront grid the shared quantization needs loses to the 1-wavefront grid of
+    // the plain GEMV by more than the separate quantization costs (K = 6144, N = 5120: 12.0 against 9.6 us; at one row
+    // 9.3 against 9.2 us, at N = 16384 16.0 against 16.4 us)
+    if (M == 1 && dot4_ok(p) && (uintptr_t)x % 16 == 0 && ldx % 8 == 0) {
+        p.x = static_cast<const uint16_t*>(x);
+        p.ldx = ldx;
+        p.xq = static_cast<int8_t*>(xq);
+        p.xs = static_cast<float*>(xs);
+        if (dtype == DT_F16) launch_dot4<f16, EPI_SMALL, true>(p);
+        else launch_dot4<bf16, EPI_SMALL, true>(p);
+        return (int)hipGetLastError();
+    }
+    const int rc = per_token_quant(x, xq, xs, M, K, ldx, dtype, stream);
+    if (rc != 0) return rc;
     dispatch_dtype_stream<EPI_SMALL>(p, dtype);
     return (int)hipGetLastError();
 }

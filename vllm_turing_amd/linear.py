@@ -9,14 +9,18 @@ weight int8 [N, K] (exposed to the matmul as its [K, N] stride-(1, K) view) and 
 import torch
 
 from .quantfuse import scaled_int8_quant
-from .w8a8 import cutlass_scaled_mm
+from .w8a8 import cutlass_scaled_mm, gemv_quant, gemv_quant_ok
 
 
 class W8A8LinearMethod:
-    """apply(layer, x, bias): per-token int8 quantization of x, int8 GEMM / GEMV, scale epilogue (+ bias)."""
+    """apply(layer, x, bias): per-token int8 quantization of x, int8 GEMM / GEMV, scale epilogue (+ bias).  At decode
+    row counts (the GEMV range) the quantization runs inside the GEMV (one launch, the same bits)."""
 
     @staticmethod
     def apply(layer, x, bias=None):
+        x2 = x.reshape(-1, x.shape[-1])
+        if gemv_quant_ok(x2, layer.weight, layer.weight_scale, bias):
+            return gemv_quant(x2, layer.weight, layer.weight_scale, bias).view(*x.shape[:-1], layer.weight.shape[0])
         x_q, x_s, _ = scaled_int8_quant(x)
         return cutlass_scaled_mm(x_q, layer.weight.t(), x_s, layer.weight_scale, x.dtype, bias)
 

@@ -153,6 +153,53 @@ def _scaled_mm_fake(out, a, b, a_scales, b_scales, bias):
     return None
 
 
+_lib_def.define("gemv_quant_(Tensor(a!) out, Tensor(b!) xq, Tensor(c!) xs, Tensor x, Tensor w, Tensor w_scale, "
+                "Tensor? bias) -> ()")
+
+
+def _gemv_quant_hip(out, xq, xs, x, w, w_scale, bias):
+    M, K = x.shape
+    N = w.shape[0]
+    if M == 0 or N == 0:
+        return
+    _check(lib().w8a8_gemv_quant(x.data_ptr(), x.stride(0), xq.data_ptr(), xs.data_ptr(), w.data_ptr(),
+                                 w_scale.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, int(w_scale.numel() > 1),
+                                 _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)), "w8a8_gemv_quant")
+
+
+torch.library.impl(_lib_def, "gemv_quant_", "CUDA")(_gemv_quant_hip)
+
+
+@torch.library.register_fake("vllm_turing_amd::gemv_quant_")
+def _gemv_quant_fake(out, xq, xs, x, w, w_scale, bias):
+    return None
+
+
+def gemv_quant_ok(x, w, w_scale, bias):
+    """Whether gemv_quant takes these operands: 1..MAX_M rows of fp16 / bf16 x with unit column stride, int8 w [N, K]
+    contiguous, K % 16 == 0, float32 scales of N or 1 elements, bias of x's dtype."""
+    if x.dim() != 2 or w.dim() != 2:
+        return False
+    M, K = x.shape
+    return (1 <= M <= min(MAX_M, GEMV_KERNEL_MAX_M) and K % 16 == 0 and x.dtype in (torch.float16, torch.bfloat16)
+            and x.stride(1) == 1 and w.dtype == torch.int8 and w.is_contiguous() and w.shape[1] == K
+            and w.data_ptr() % 16 == 0 and w_scale.dtype == torch.float32 and w_scale.is_contiguous()
+            and w_scale.numel() in (1, w.shape[0])
+            and (bias is None or (bias.dtype == x.dtype and bias.is_contiguous() and bias.numel() == w.shape[0])))
+
+
+def gemv_quant(x, w, w_scale, bias=None):
+    """Decode W8A8 linear from 16-bit activations with the quantization fused into the GEMV: x fp16 / bf16 [M, K]
+    (M <= 12), w int8 [N, K], w_scale float32 [N, 1] or [1] -> out [M, N] in x's dtype, bit-identical to
+    per_token_quant followed by cutlass_scaled_mm (which runs w8a8_gemv at these M)."""
+    M, K = x.shape
+    out = torch.empty((M, w.shape[0]), dtype=x.dtype, device=x.device)
+    xq = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    xs = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    torch.ops.vllm_turing_amd.gemv_quant_(out, xq, xs, x, w, w_scale, bias)
+    return out
+
+
 def cutlass_scaled_mm(a, b, scale_a, scale_b, out_dtype, bias=None):
     """vLLM's cutlass_scaled_mm signature (vllm_turing/w8a8.py:136-147): a int8 [..., K], b int8 [K, N] (the stride-
     (1, K) view of the [N, K] weight), scale_a float32 [M, 1] or [1], scale_b float32 [N, 1] or [1] -> out [..., N]."""
