@@ -416,14 +416,15 @@ def bench_headline(torch, L, st, dev, args):
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def read(i):
-        rc = L.hbm_read(ws[i % copies].data_ptr(), N * K, sink.data_ptr(), st())
+        rc = L.hbm_read(ws[i % copies].data_ptr(), N, K, sink.data_ptr(), st())
         if rc != 0:
             raise RuntimeError(f"hbm_read {rc}")
 
     ms_read, _ = graph_time(torch, read, 4 * copies, args.steps, args.warmup)
     read_gbs = N * K / (ms_read * 1e-3) / 1e9
-    read_ceiling = {"workload": f"read-only stream of the same {copies} rotated {N * K / 1e6:.0f} MB weight copies "
-                                f"(16-byte non-temporal loads, the GEMV's load path, no math)",
+    read_ceiling = {"workload": f"the M=1 GEMV's weight stream without its math over the same {copies} rotated "
+                                f"{N * K / 1e6:.0f} MB weight copies (its grid, 1 KB non-temporal row loads, next row "
+                                f"in flight)",
                     "us": round(ms_read * 1e3, 2), "gbs": round(read_gbs, 1),
                     "frac": round(read_gbs / HBM_PEAK_GBS, 4), "gemv_over_read": round(gemv_gbs / read_gbs, 4)}
     print(f"[bench] read ceiling {ms_read * 1e3:.2f} us/launch, {read_gbs:.0f} GB/s", file=sys.stderr, flush=True)

@@ -141,12 +141,13 @@ int silu_table(void* out, int dtype, void* stream);
  * reference.  Returns -1 on bad arguments, else the HIP launch error. */
 int f32_to_16(const void* x, void* out, long n, int dtype, void* stream);
 
-/* Test export: a read-only stream of `bytes` bytes of src (16-byte aligned, bytes % 16 == 0) through the weight-
- * streaming GEMV's load path (16-byte non-temporal loads, 1 KB per wavefront instruction), the data discarded: the
- * achievable read rate the GEMV is measured against.  sink: one int of device memory, written only if the XOR of all
- * words read equals 0x5a3c96e1.  No counterpart in the reference.  Returns -1 on bad arguments, else the launch
+/* Test export: the M = 1 decode GEMV's weight stream without its math: rows x K bytes of src (16-byte aligned,
+ * K % 16 == 0, K <= 17408) read exactly as w8a8_gemv reads its weights at one activation row (one-wavefront
+ * workgroups of three rows, 1 KB per wavefront instruction, non-temporal loads, the next row's loads in flight) and
+ * discarded: the read rate the GEMV is measured against.  sink: one int of device memory, written only if the XOR of
+ * all words read equals 0x5a3c96e1.  No counterpart in the reference.  Returns -1 on bad arguments, else the launch
  * error. */
-int hbm_read(const void* src, long bytes, void* sink, void* stream);
+int hbm_read(const void* src, int rows, int K, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -99,9 +99,10 @@ def test_argument_validation_codes(L):
     assert L.w8a8_gemv_quant(None, 64, 16, 16, 16, 16, None, 16, 4, 64, 64, 1, 0, None) == -1    # x
     assert L.w8a8_gemv_quant(16, 64, 16, 16, 16, 16, None, 16, 4, 64, 72, 1, 0, None) == -1      # K % 16
     assert L.w8a8_gemv_quant(16, 64, 8, 16, 16, 16, None, 16, 4, 64, 64, 1, 0, None) == -1       # xq aligned
-    assert L.hbm_read(None, 1024, 16, None) == -1
-    assert L.hbm_read(16, 1000, 16, None) == -1                                    # bytes % 16
-    assert L.hbm_read(8, 1024, 16, None) == -1                                     # 16-byte aligned
+    assert L.hbm_read(None, 4, 1024, 16, None) == -1
+    assert L.hbm_read(16, 4, 1000, 16, None) == -1                                 # K % 16
+    assert L.hbm_read(16, 4, 17424, 16, None) == -1                                # K <= 17408
+    assert L.hbm_read(8, 4, 1024, 16, None) == -1                                  # 16-byte aligned
     assert L.silu_table(16, 4, None) == -1                                         # 0..3
     assert L.ar8_quant(16, 16, 100, None) == -1                                 # n % 128
     assert L.ar8_quant(8, 16, 128, None) == -1                                  # x 16-byte aligned

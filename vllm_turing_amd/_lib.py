@@ -30,7 +30,7 @@ SIGNATURES = {
     "silu_table": [_vp, _i, _vp],
     "silu_mul_quant_path": [_vp] * 3 + [_i] * 4 + [_vp],
     "f32_to_16": [_vp, _vp, _l, _i, _vp],
-    "hbm_read": [_vp, _l, _vp, _vp],
+    "hbm_read": [_vp, _i, _i, _vp, _vp],
 }
 
 _lib = None

@@ -1718,28 +1718,44 @@ extern "C" int w8a8_i32(const void* a, const void* w, void* acc, int M, int N, i
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// hbm_read: a read-only stream of a buffer (the ceiling the weight-streaming GEMV is measured against)
+// hbm_read: the M = 1 GEMV's weight stream without its math (the ceiling the GEMV is measured against)
 // ---------------------------------------------------------------------------------------------------------------------
-// The GEMV's loads without its math: 16 bytes per lane, non-temporal, each wavefront instruction 1 KB contiguous, four
-// in flight per lane, grid-strided over HBM_READ_BLOCKS_PER_CU workgroups of 256 per CU.  The words read are XORed
-// together and the result is stored only if it equals a value no real input produces in practice, so the kernel
-// writes nothing while the loads cannot be removed.
-constexpr int HBM_READ_BLOCKS_PER_CU = 8, HBM_READ_UNROLL = 4;
-
-__global__ void __launch_bounds__(256) hbm_read_kernel(const v4i* __restrict__ src, long n16, int* __restrict__ sink) {
-    const long stride = (long)gridDim.x * blockDim.x;
-    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+// Rows of K bytes exactly as gemv_dot4_kernel reads them at one activation row: one-wavefront workgroups, rows
+// grid-strided over ceil(rows / 3) wavefronts, each wavefront instruction 1 KB of one row (lane l: 16-byte chunks l,
+// l + 64, ...), non-temporal, the next row's loads issued before the current row is consumed.  The words are XORed
+// and the result stored only if it equals a value no real input produces in practice, so nothing is written while
+// the loads cannot be removed.
+template <int CH>
+__global__ void __launch_bounds__(64) hbm_read_kernel(const int8_t* __restrict__ src, int rows, int K,
+                                                      int* __restrict__ sink) {
+    const int lane = threadIdx.x & 63, nw = gridDim.x, wid = blockIdx.x, K16 = K >> 4;
+    if (wid >= rows) return;
+    v4i buf[2][CH];
+    auto load = [&](int b, int r) {
+        const int8_t* row = src + (long)min(r, rows - 1) * K;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) buf[b][j] = wload<true>(row + min(lane + 64 * j, K16 - 1) * 16);
+    };
     int x = 0;
-    for (; i + (HBM_READ_UNROLL - 1) * stride < n16; i += HBM_READ_UNROLL * stride) {
-        v4i v[HBM_READ_UNROLL];
+    auto use = [&](int b) {
 #pragma unroll
-        for (int u = 0; u < HBM_READ_UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
-#pragma unroll
-        for (int u = 0; u < HBM_READ_UNROLL; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        for (int j = 0; j < CH; ++j) x ^= buf[b][j].x ^ buf[b][j].y ^ buf[b][j].z ^ buf[b][j].w;
+    };
+    const int cnt = (rows - 1 - wid) / nw + 1;
+    load(0, wid);
+    int k = 0;
+    for (; k + 2 < cnt; k += 2) {                        // peeled as gemv_dot4_kernel: no load under a condition
+        load(1, wid + (k + 1) * nw);
+        use(0);
+        load(0, wid + (k + 2) * nw);
+        use(1);
     }
-    for (; i < n16; i += stride) {
-        const v4i v = __builtin_nontemporal_load(src + i);
-        x ^= v.x ^ v.y ^ v.z ^ v.w;
+    if (k + 1 < cnt) {
+        load(1, wid + (k + 1) * nw);
+        use(0);
+        use(1);
+    } else {
+        use(0);
     }
     if (x == 0x5a3c96e1) sink[0] = x;
 }
@@ -1876,15 +1892,23 @@ extern "C" int w8a16_mma(const void* x, const void* w, const void* s, const void
     return 0;
 }
 
-// Test export: stream `bytes` bytes of src (16-byte aligned, bytes % 16 == 0) through the GEMV's load path and discard
-// them (sink: one int, written only in the improbable case described at hbm_read_kernel).  No counterpart in the
-// reference.  Returns -1 on bad arguments, else the launch error.
-extern "C" int hbm_read(const void* src, long bytes, void* sink, void* stream) {
-    if (!src || !sink || bytes < 16 || bytes % 16 != 0 || (uintptr_t)src % 16 != 0) return -1;
-    const long n16 = bytes / 16;
-    const long need = (n16 + 255) / 256;
-    const long cap = (long)cu_count() * HBM_READ_BLOCKS_PER_CU;
-    hbm_read_kernel<<<(int)(need < cap ? need : cap), 256, 0, (hipStream_t)stream>>>(static_cast<const v4i*>(src), n16,
-                                                                                     static_cast<int*>(sink));
+// Test export: stream rows x K bytes of src (16-byte aligned, K % 16 == 0, K <= 17408) through the M = 1 GEMV's
+// load path and discard them (sink: one int, written only in the improbable case described at hbm_read_kernel).  No
+// counterpart in the reference.  Returns -1 on bad arguments, else the launch error.
+extern "C" int hbm_read(const void* src, int rows, int K, void* sink, void* stream) {
+    if (!src || !sink || rows < 1 || K < 16 || K % 16 != 0 || (uintptr_t)src % 16 != 0 || (long)rows * K >= (1L << 40))
+        return -1;
+    const int ch = dot4_chunks(K);
+    const int waves = (rows + DOT4_ROWS_PER_WAVE - 1) / DOT4_ROWS_PER_WAVE;
+    const int8_t* s8 = static_cast<const int8_t*>(src);
+    int* sk = static_cast<int*>(sink);
+    hipStream_t st = (hipStream_t)stream;
+    switch (ch) {
+#define W8_CASE(C) case C: hbm_read_kernel<C><<<waves, 64, 0, st>>>(s8, rows, K, sk); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8) W8_CASE(10)
+        W8_CASE(12) W8_CASE(14) W8_CASE(17)
+#undef W8_CASE
+        default: return -1;
+    }
     return (int)hipGetLastError();
 }
