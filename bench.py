@@ -30,8 +30,9 @@ Also reported:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--sections headline,mlp,stack]
        python bench.py --traffic     (a short fixed launch sequence for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs:
-                                      10 GEMVs over 5 weight copies, a 256 MB device copy for calibrating the counters,
-                                      3 GEMMs, 3 per-token quants, 3 SiLU*up quants; prints nothing else)
+                                      10 GEMVs, 10 fused-quant GEMVs and 10 weight-stream reads over 5 weight copies,
+                                      a 256 MB device copy for calibrating the counters, 3 GEMMs, 3 per-token quants,
+                                      3 SiLU*up quants; prints nothing else)
 """
 import argparse
 import json
@@ -190,6 +191,13 @@ def traffic_sequence(torch, L, st, dev):
     for i in range(10):
         L.w8a8_gemv(xq.data_ptr(), ws[i % 5].data_ptr(), xs.data_ptr(), sw.data_ptr(), None, out.data_ptr(), M, N, K,
                     1, 1, 0, st())
+    x16 = (torch.randn(M, K, device=dev, generator=g) * 3).to(torch.float16)
+    for i in range(10):
+        L.w8a8_gemv_quant(x16.data_ptr(), K, xq.data_ptr(), xs.data_ptr(), ws[i % 5].data_ptr(), sw.data_ptr(), None,
+                          out.data_ptr(), M, N, K, 1, 0, st())
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    for i in range(10):
+        L.hbm_read(ws[i % 5].data_ptr(), N, K, sink.data_ptr(), st())
     torch.cuda.synchronize()
     del ws
     src = torch.ones(256 * 1024 * 1024, dtype=torch.uint8, device=dev)   # calibration: 256 MiB read + write
