@@ -230,16 +230,38 @@ def traffic_sequence(torch, L, st, dev):
     torch.cuda.synchronize()
 
 
+_WS = []
+
+
+def workspace(torch, dev):
+    """The prefill GEMM's K-split workspace (zeroed once; every call leaves its counters zero), sized for any shape:
+    4 KB of tile counters + 256 KB per CU, as the package's layers hold one per device and stream."""
+    if not _WS:
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        _WS.append(torch.zeros(4096 + cus * 262144, dtype=torch.uint8, device=dev))
+    return _WS[0]
+
+
+def scaled_mm_ws(L, st, a_q, w, a_s, sw, bias, out, M, N, K, dtype_code):
+    """The large-M W8A8 GEMM as the package runs it: w8a8_scaled_mm_ws with the workspace (the whole rounds of super
+    tiles, then the last partial round split over K)."""
+    ws = _WS[0]
+    return L.w8a8_scaled_mm_ws(a_q.data_ptr(), w.data_ptr(), a_s.data_ptr(), sw.data_ptr(),
+                               None if bias is None else bias.data_ptr(), out.data_ptr(), M, N, K, 1, 1, dtype_code,
+                               ws.data_ptr(), ws.numel(), st())
+
+
 def linear_launch(L, st, a_q, a_s, w, sw, out, M, N, K, dtype_code):
     """One W8A8 projection through the entry point the reference's dispatch picks for M (no bias): the streaming
-    GEMV for M <= 12, the MMA variant for M <= 32, the prefill GEMM above."""
+    GEMV for M <= 12, the MMA variant for M <= 32, the prefill GEMM above (w8a8_big's kernels, through the workspace
+    entry as the package's layers call them)."""
     args = (a_q.data_ptr(), w.data_ptr(), a_s.data_ptr(), sw.data_ptr())
     if M <= 12:
         rc = L.w8a8_gemv(*args, None, out.data_ptr(), M, N, K, 1, 1, dtype_code, st())
     elif M <= 32:
         rc = L.w8a8_mma(*args, None, out.data_ptr(), M, N, K, 1, 1, dtype_code, st())
     else:
-        rc = L.w8a8_big(*args, out.data_ptr(), M, N, K, dtype_code, st())
+        rc = scaled_mm_ws(L, st, a_q, w, a_s, sw, None, out, M, N, K, dtype_code)
     if rc != 0:
         raise RuntimeError(f"W8A8 linear M={M} N={N} K={K}: {rc}")
 
@@ -480,10 +502,9 @@ def bench_headline(torch, L, st, dev, args):
     outg = torch.empty(Mg, Ng, dtype=torch.bfloat16, device=dev)
 
     def gemm(i):
-        rc = L.w8a8_scaled_mm(a_q.data_ptr(), wgs[i % gcopies].data_ptr(), a_s.data_ptr(), swg.data_ptr(),
-                              bias.data_ptr(), outg.data_ptr(), Mg, Ng, Kg, 1, 1, 1, st())
+        rc = scaled_mm_ws(L, st, a_q, wgs[i % gcopies], a_s, swg, bias, outg, Mg, Ng, Kg, 1)
         if rc != 0:
-            raise RuntimeError(f"w8a8_scaled_mm {rc}")
+            raise RuntimeError(f"w8a8_scaled_mm_ws {rc}")
 
     print(f"[bench] GEMM M={Mg} K={Kg} N={Ng}", file=sys.stderr, flush=True)
     # 2 s of back-to-back GEMMs first, untimed: the clock sample, and the warm-up that lets the clock settle (the
@@ -502,10 +523,9 @@ def bench_headline(torch, L, st, dev, args):
         outo = torch.empty(Mo, Ng, dtype=torch.bfloat16, device=dev)
 
         def gemm_o(i, Mo=Mo, outo=outo):
-            rc = L.w8a8_scaled_mm(a_q.data_ptr(), wgs[i % gcopies].data_ptr(), a_s.data_ptr(), swg.data_ptr(),
-                                  bias.data_ptr(), outo.data_ptr(), Mo, Ng, Kg, 1, 1, 1, st())
+            rc = scaled_mm_ws(L, st, a_q, wgs[i % gcopies], a_s, swg, bias, outo, Mo, Ng, Kg, 1)
             if rc != 0:
-                raise RuntimeError(f"w8a8_scaled_mm M={Mo}: {rc}")
+                raise RuntimeError(f"w8a8_scaled_mm_ws M={Mo}: {rc}")
 
         ms_o, _ = graph_time(torch, gemm_o, 2 * gcopies, 8 * gcopies, 2 * gcopies)
         tops_o = 2.0 * Mo * Ng * Kg / (ms_o * 1e-3) / 1e12
@@ -675,6 +695,7 @@ def main():
     torch.cuda.set_device(0)
     L = _lib.lib()
     st = lambda: torch.cuda.current_stream().cuda_stream
+    workspace(torch, dev)
     if args.traffic:
         traffic_sequence(torch, L, st, dev)
         return

@@ -53,6 +53,24 @@ int w8a8_big(const void* A, const void* W, const void* sa, const void* sw, void*
 int w8a8_scaled_mm(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out, int M,
                    int N, int K, int sa_rows, int sw_rows, int dtype, void* stream);
 
+/* w8a8_scaled_mm (and so w8a8_big, which is its no-bias per-row / per-column case) with a caller workspace for the
+ * prefill GEMM's K split: when the 256 x 256 super tiles leave a last partial round of at most half the CUs, each of
+ * those tiles runs as 2..8 K pieces whose int32 partial sums meet in the workspace (the last piece to finish adds
+ * them and runs the epilogue; the results are bit-identical to w8a8_scaled_mm's).  workspace: 16-byte aligned,
+ * ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K) (it may be null when that is 0); its first 4 KB (tile counters) must be
+ * zero before the first call, and every call leaves them zero.  Calls that share a workspace must not overlap.
+ * dtype 2 writes the raw int32 accumulators acc [M, N] to out (sa, sw, bias unused; for checking).  Returns -1 on bad
+ * arguments (a missing or too small workspace included), else the HIP error code of the launches.
+ * No counterpart in the reference, whose w8a8_big rejects a workspace (vllm_turing/csrc/w8a8_big.cu:57-59); this
+ * serves the same callers as w8a8_big and w8a8_scaled_mm (vllm_turing/w8a8.py:92-101,117). */
+int w8a8_scaled_mm_ws(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out,
+                      int M, int N, int K, int sa_rows, int sw_rows, int dtype, void* workspace, long ws_bytes,
+                      void* stream);
+
+/* Workspace bytes w8a8_scaled_mm_ws takes for M x N x K on the current device: 0 when the shape does not split, at
+ * most 4 KB + 256 KB per CU; -1 for M, N < 1 or K < 16. */
+long w8a8_scaled_mm_ws_size(int M, int N, int K);
+
 /* Dynamic symmetric per-token int8 quantization: scales[m] = absmax_m / 127,
  * q[m, k] = clamp(rint(float(x[m, k]) * (127 / absmax_m)), -128, 127); a zero row gives q = 0 and scale 0.
  * x: [M, K] fp16/bf16 with row stride ldx elements; q: [M, K] int8 contiguous; scales: [M] float32.

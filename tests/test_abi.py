@@ -17,7 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def header_symbols():
     txt = open(os.path.join(ROOT, "include", "w8a8_mi355.h")).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return re.findall(r"^\s*int\s+(\w+)\s*\(", txt, flags=re.M)
+    return re.findall(r"^\s*(?:int|long)\s+(\w+)\s*\(", txt, flags=re.M)
 
 
 @pytest.fixture(scope="module")
@@ -57,6 +57,18 @@ def test_argument_validation_codes(L):
     assert L.w8a8_big(16, 16, 0, 0, 0, 64, 24, 64, 0, None) == 1                  # N % 16
     assert L.w8a8_big(16, 16, 0, 0, 0, 64, 64, 72, 0, None) == 1                  # K % 16
     assert L.w8a8_scaled_mm(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
+    # w8a8_scaled_mm_ws: a shape that splits needs its workspace (missing, too small, misaligned: -1)
+    need = L.w8a8_scaled_mm_ws_size(512, 12288, 5120)
+    assert need > 4096 and (need - 4096) % (256 * 1024) == 0
+    assert L.w8a8_scaled_mm_ws(16, 16, 0, 0, None, 0, 512, 12288, 5120, 1, 1, 1, None, 0, None) == -1
+    assert L.w8a8_scaled_mm_ws(16, 16, 0, 0, None, 0, 512, 12288, 5120, 1, 1, 1, 4096, need - 1, None) == -1
+    assert L.w8a8_scaled_mm_ws(16, 16, 0, 0, None, 0, 512, 12288, 5120, 1, 1, 1, 4100, need, None) == -1
+    assert L.w8a8_scaled_mm_ws(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None, 0, None) == -1
+    assert L.w8a8_scaled_mm_ws(16, 16, 0, 0, None, 0, 64, 64, 64, 1, 1, 3, None, 0, None) == -1   # dtype 0..2
+    assert L.w8a8_scaled_mm_ws_size(0, 64, 64) == -1 and L.w8a8_scaled_mm_ws_size(64, 64, 8) == -1
+    assert L.w8a8_scaled_mm_ws_size(200, 1024, 5120) == 0       # a mid-M shape: no split
+    assert L.w8a8_scaled_mm_ws_size(4096, 12288, 5120) == 0     # 768 super tiles: whole rounds on 256 CUs
+    assert L.w8a8_scaled_mm_ws_size(512, 12288, 512) == 0       # 4 K stages: pieces would be under 4 stages
     assert L.w8a8_i32(16, 16, 0, 65, 64, 64, 0, None) == -1                       # streaming kernel: M <= 64
     assert L.w8a8_i32(16, 16, 0, 6, 64, 64, 2, None) == -1                       # VALU kernel: M <= 5
     assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # K <= 17408 at one row

@@ -701,6 +701,127 @@ def test_scaled_mm_bits(L, M, N, K, dt, with_bias, per_tensor, order):
     assert not over.any(), f"{int(over.sum())} outputs further than one 16-bit ulp from the exact value"
 
 
+# ---------------------------------------------------------------------------------------------------------------------
+# the prefill GEMM's K split (w8a8_scaled_mm_ws): the last partial round of super tiles as K pieces met in a workspace
+# ---------------------------------------------------------------------------------------------------------------------
+SPLIT_SHAPES = [
+    (512, 12288, 5120),     # 96 super tiles x 2 pieces
+    (2048, 12288, 5120),    # 256 whole tiles, then 128 x 2
+    (4096, 5120, 17408),    # 256 whole, then 64 x 4 (the MLP down projection)
+    (1000, 3000, 2064),     # 48 x 4, ragged M, N and K (K % 128 = 16: the last stage zero-filled)
+    (768, 8192, 1024),      # 96 x 2 at 8 stages
+    (300, 1000, 5120),      # 8 x 8
+    (4096, 17152, 2048),    # 1072 tiles: 768 whole in a launch of their own, 256 whole + 48 x 4 in the next
+]
+
+
+def split_ws(L, M, N, K):
+    need = L.w8a8_scaled_mm_ws_size(M, N, K)
+    assert need > 4096, (M, N, K, need)                  # the shape does split
+    return torch.zeros(need, dtype=torch.uint8, device=DEV)
+
+
+def ws_call(L, a, w, sa, sw, bias, out, ws, dcode, sa_rows=1, sw_rows=1):
+    M, K = a.shape
+    N = w.shape[0]
+    ptr = (lambda t: None if t is None else t.data_ptr())
+    rc = L.w8a8_scaled_mm_ws(a.data_ptr(), w.data_ptr(), ptr(sa), ptr(sw), ptr(bias), out.data_ptr(), M, N, K,
+                             sa_rows, sw_rows, dcode, ws.data_ptr(), ws.numel(), stream())
+    assert rc == 0, rc
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_split_i32(L, M, N, K):
+    """Raw int32 accumulators of the split path whole against the exact products; the tile counters are back at zero
+    and a second call on the same workspace gives the same result."""
+    say(f"split i32 M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    ws = split_ws(L, M, N, K)
+    ad, wd = a.to(DEV), w.to(DEV)
+    acc = torch.empty(M, N, dtype=torch.int32, device=DEV)
+    ws_call(L, ad, wd, None, None, None, acc, ws, 2)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(oracle.gemm_i32(a.numpy(), w.numpy())) if M * N * K < 2e9 else torch._int_mm(a, w.t())
+    got = acc.cpu()
+    assert torch.equal(got, ref), f"{int((got != ref).sum())} of {ref.numel()} int32 differ"
+    assert int(ws[:4096].count_nonzero()) == 0
+    acc.fill_(0)
+    ws_call(L, ad, wd, None, None, None, acc, ws, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,dt,with_bias", [(512, 12288, 5120, torch.bfloat16, True),
+                                                (1000, 3000, 2064, torch.float16, False),
+                                                (2048, 12288, 5120, torch.float16, True)])
+def test_split_bits(L, M, N, K, dt, with_bias):
+    """16-bit outputs of the split path bit-identical to w8a8_scaled_mm's (no workspace) and to the oracle's large-M
+    epilogue of the exact products."""
+    say(f"split bits M={M} N={N} K={K} {dt} bias={with_bias}")
+    g = torch.Generator().manual_seed(M + 7 * N + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    sa = torch.rand(M, generator=g) * 1e-2
+    sw = torch.rand(N, generator=g) * 1e-3
+    bias = torch.randn(N, generator=g).to(dt) if with_bias else None
+    ad, wd, sad, swd = a.to(DEV), w.to(DEV), sa.to(DEV), sw.to(DEV)
+    bd = None if bias is None else bias.to(DEV)
+    ws = split_ws(L, M, N, K)
+    out = torch.empty(M, N, dtype=dt, device=DEV)
+    plain = torch.empty(M, N, dtype=dt, device=DEV)
+    ws_call(L, ad, wd, sad, swd, bd, out, ws, code(dt))
+    assert L.w8a8_scaled_mm(ad.data_ptr(), wd.data_ptr(), sad.data_ptr(), swd.data_ptr(),
+                            None if bd is None else bd.data_ptr(), plain.data_ptr(), M, N, K, 1, 1, code(dt),
+                            stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), bits(plain))
+    acc = torch._int_mm(a, w.t())
+    ref = oracle.epilogue(acc.numpy(), sa.numpy(), sw.numpy(), None if bias is None else bits(bias), code(dt),
+                          oracle.ORDER_LARGE_M)
+    got = bits(out)
+    assert np.array_equal(got, ref), f"{int((got != ref).sum())} of {got.size} differ"
+
+
+def test_split_shared_workspace_and_graph(L):
+    """One workspace for calls of different shapes in a row, then the split path captured in a HIP graph and replayed
+    three times with eager work in between: every result equal to the eager one."""
+    say("split shared workspace + graph replay")
+    shapes = [(1000, 3000, 2064), (300, 1000, 5120), (1000, 3000, 2064)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ws = torch.zeros(4096 + cus * 262144, dtype=torch.uint8, device=DEV)
+    g = torch.Generator().manual_seed(5)
+    ops = []
+    for M, N, K in shapes:
+        a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+        w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+        ref = torch.from_numpy(oracle.gemm_i32(a.numpy(), w.numpy()))
+        ops.append((a.to(DEV), w.to(DEV), torch.empty(M, N, dtype=torch.int32, device=DEV), ref))
+    for a, w, acc, ref in ops:
+        ws_call(L, a, w, None, None, None, acc, ws, 2)
+    torch.cuda.synchronize()
+    for a, w, acc, ref in ops:
+        assert torch.equal(acc.cpu(), ref)
+    a, w, acc, ref = ops[0]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        ws_call(L, a, w, None, None, None, acc, ws, 2)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        acc.fill_(-1)
+        b2, w2, acc2, ref2 = ops[1]
+        ws_call(L, b2, w2, None, None, None, acc2, ws, 2)     # eager use of the same workspace between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(acc.cpu(), ref), rep
+        assert torch.equal(acc2.cpu(), ref2), rep
+    assert int(ws[:4096].count_nonzero()) == 0
+
+
 GEMV_QUANT_CASES = [
     # M, N, K, dtype, ldx extra, bias, zero row
     (1, 5120, 6144, torch.bfloat16, 0, False, False),     # out_proj / o_proj at M = 1

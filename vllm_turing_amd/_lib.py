@@ -14,6 +14,8 @@ SIGNATURES = {
     "w8a8_mma": [_vp] * 6 + [_i] * 6 + [_vp],
     "w8a8_big": [_vp] * 5 + [_i] * 4 + [_vp],
     "w8a8_scaled_mm": [_vp] * 6 + [_i] * 6 + [_vp],
+    "w8a8_scaled_mm_ws": [_vp] * 6 + [_i] * 6 + [_vp, _l, _vp],
+    "w8a8_scaled_mm_ws_size": [_i] * 3,
     "w8a8_gemv_quant": [_vp, _l, _vp, _vp] + [_vp] * 4 + [_i] * 5 + [_vp],
     "per_token_quant": [_vp] * 3 + [_i, _i, _l, _i, _vp],
     "silu_mul_quant": [_vp] * 3 + [_i] * 2 + [_vp],
@@ -32,6 +34,7 @@ SIGNATURES = {
     "f32_to_16": [_vp, _vp, _l, _i, _vp],
     "hbm_read": [_vp, _i, _i, _vp, _vp],
 }
+RESTYPES = {"w8a8_scaled_mm_ws_size": _l}
 
 _lib = None
 
@@ -44,7 +47,7 @@ def lib():
         for name, argtypes in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         _lib = L
     return _lib
 

@@ -634,11 +634,21 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 // so every region has at least two slots to land, and before each barrier a wavefront waits (vmcnt, exact counts,
 // vector memory operations retire in order) for its own loads of the regions read in the next slot.  No group refills
 // a region from its memory phase.  Group 0 begins its epilogue while group 1 computes the last stage.
-template <typename T, int EPI, bool KFULL, int GM = GROUP_M, bool PRIO = true>
+//
+// SPLITK: workgroups 0 .. full - 1 take whole super tiles t_base + 0 .. full - 1 as above, and the rest `splits` K
+// pieces of each of the next (gridDim.x - full) / splits tiles (workgroup u of that part: piece u / rem of tile
+// t_base + full + u % rem, so that the workgroups of one XCD share K ranges).  Piece p runs stages
+// [p nk / splits, (p + 1) nk / splits), stores its int32 accumulators to its slot of the workspace and arrives at its
+// tile's counter; the last to arrive adds the other pieces' slots to its own accumulators (integer sums: the result is
+// the same in any order) and runs the epilogue, then sets the counter back to zero.  No workgroup waits for another.
+constexpr int SPLIT_HEAD_INTS = 1024;                    // workspace: tile counters, then the slots
+constexpr int SPLIT_SLOT_INTS = SUPER * SUPER;           // one super tile of int32 accumulators (256 KB)
+template <typename T, int EPI, bool KFULL, bool SPLITK = false, int GM = GROUP_M, bool PRIO = true>
 __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                       const float* __restrict__ sa, const float* __restrict__ sw,
                                                       const uint16_t* __restrict__ bias, void* __restrict__ out,
-                                                      int M, int N, int K, int sa_rows, int sw_rows, int t_base) {
+                                                      int M, int N, int K, int sa_rows, int sw_rows, int t_base,
+                                                      int splits, int full, int* __restrict__ ws) {
     extern __shared__ v4i ldsx[];
     constexpr int WM = 2, WN = 4, FM = 4, FN = 2, KB = 128, NS = 2;
     using Cfg = GemmCfg<WM, WN, FM, FN, KB, NS>;
@@ -650,10 +660,22 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__
 
     // tile mapping of gemm_kernel (XCD-aware remap, raster groups of GM super-tile rows)
     const int TM = (M + SUPER - 1) / SUPER, TN = (N + SUPER - 1) / SUPER;
-    const int nb = gridDim.x, per = nb >> 3;
-    int u = blockIdx.x;
+    // with SPLITK the first `full` workgroups take whole tiles t_base + 0 .. full - 1 (dispatched first, one round
+    // over the CUs) and the rest the K pieces of the next tiles, each part remapped within itself
+    const bool split_role = SPLITK && (int)blockIdx.x >= full;
+    const int base = split_role ? full : 0, cnt = SPLITK ? (split_role ? gridDim.x - full : full) : gridDim.x;
+    const int per = cnt >> 3;
+    int u = blockIdx.x - base;
     if (u < per * 8) u = (u & 7) * per + (u >> 3);
-    const int t = t_base + u;
+    int nk = (K + KB - 1) / KB, kst0 = 0, piece = 0, rt = u;   // stages of this workgroup, its first, its K piece
+    if (split_role) {
+        const int rem = cnt / splits;
+        piece = u / rem;
+        rt = u % rem;
+        kst0 = piece * nk / splits;
+        nk = (piece + 1) * nk / splits - kst0;           // >= 1: the host takes splits <= the stage count
+    }
+    const int t = t_base + base + rt;
     const int gsz = GM * TN, gi = t / gsz, first_m = gi * GM;
     const int gm = min(TM - first_m, GM);
     const int m0 = (first_m + (t % gsz) % gm) * SUPER, n0 = ((t % gsz) / gm) * SUPER;
@@ -675,7 +697,7 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__
         const int blk = grp == 0 ? (q < 4 ? 16 : 0) + gw * 4 + (q & 3) : gw * 8 + q;   // block within A or W
         const int lrow = (grp == 0 ? 0 : BM) + blk * RPB;                                 // staged row in the buffer
         const unsigned base = (org + (unsigned)(blk * RPB)) * (unsigned)K;
-        const int k0 = st * KB;
+        const int k0 = (kst0 + st) * KB;
         unsigned voff = base + ((q & 1) ? lane1 : lane0);
         if constexpr (!KFULL) {                          // a K chunk past the end reads as zeros
             if (k0 + ((q & 1) ? ch1 : ch0) * 16 >= K) voff = 0x7fffffffu;
@@ -748,7 +770,6 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__
     };
     constexpr int LGKM0 = 0xc07f;
 
-    const int nk = (K + KB - 1) / KB;
     // prologue: stage 0 whole (group 0: A1 and A0, group 1: W), group 0 also A0 of stage 1, group 1 also W of stage 1
 #pragma unroll
     for (int q = 0; q < 8; ++q) load(q, 0);
@@ -798,6 +819,51 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__
     // Epilogue: group 0 starts while group 1 computes the last stage (slot 2 nk).  Every load has landed and the last
     // reads of the stage buffers ended before the barrier closing slot 2 nk - 1, and each wavefront transposes through
     // its own LDS region, so no further barrier is needed (both groups passed 2 nk + 1).
+
+    if (split_role) {
+        // The slots are written and read with agent-coherent accesses (the sc1 form the compiler gives relaxed
+        // agent-scope atomic stores and loads), so a piece's slot is visible on every XCD once its stores complete,
+        // without an L2 write-back or invalidation (the compiler's agent-scope fences do both, for the whole L2, and
+        // made the K-split slower than no split).  Each wavefront waits for its own stores; the barrier then orders
+        // them before the tile's arrival, and the reads of the last piece after it.  Layout per piece: 32 KB per
+        // wavefront in its fragment order, 1 KB per store instruction (lane l at 16 l).
+        constexpr int WAVE_V4 = FM * FN * 4 * 64;
+        constexpr int CPOL_SC1 = 16;
+        const long tile_slot = (long)rt * splits;        // (slots and counters indexed from the first split tile)
+        const __amdgpu_buffer_rsrc_t rsp =
+            make_rsrc(ws + SPLIT_HEAD_INTS + tile_slot * SPLIT_SLOT_INTS, (long)splits * SPLIT_SLOT_INTS * 4);
+        auto voff = [&](int q, int f, int c) { return ((q * 8 + wave) * WAVE_V4 + (f * 4 + c) * 64 + lane) * 16; };
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        v4i{acc[i][j][4 * c], acc[i][j][4 * c + 1], acc[i][j][4 * c + 2], acc[i][j][4 * c + 3]}, rsp,
+                        voff(piece, i * FN + j, c), 0, CPOL_SC1);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __shared__ int last;
+        __syncthreads();
+        if (tid == 0)
+            last = __hip_atomic_fetch_add(ws + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+        __syncthreads();
+        if (!last) return;
+        for (int q = 0; q < splits; ++q) {
+            if (q == piece) continue;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsp, voff(q, i * FN + j, c), 0, CPOL_SC1);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][j][4 * c + e] += v[e];
+                    }
+        }
+        if (tid == 0) __hip_atomic_store(ws + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     const int mb = m0 + grp * WTM, nbw = n0 + gw * WTN;
     if constexpr (EPI == EPI_I32) {
@@ -1243,6 +1309,9 @@ struct Args {
     long ldx = 0;
     int8_t* xq = nullptr;
     float* xs = nullptr;
+    // the prefill GEMM's K-split remainder: a workspace of tile counters (zero between calls) and accumulator slots
+    int* ws = nullptr;
+    long ws_bytes = 0;
 };
 
 // One to five activation rows: the VALU kernel (measured against the LDS-ring MFMA kernel with ordinary loads: 16.8
@@ -1485,24 +1554,26 @@ constexpr int LONG_ROUNDS = 6;
 #define W8_GEMM_PP 1
 #endif
 // The main configuration with its wavefront groups in alternating roles (gemm_pp_kernel).
+template <typename T, int EPI, bool KFULL, bool SPLITK>
+static void launch_gemm_pp_k(const Args& p, int t_base, int blocks, int splits, int full) {
+    using G = GemmCfg<MainCfg::WM, MainCfg::WN, MainCfg::FM, MainCfg::FN, MainCfg::KB, MainCfg::NS>;
+    const void* kern = reinterpret_cast<const void*>(&gemm_pp_kernel<T, EPI, KFULL, SPLITK>);
+    static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+    (void)attr;
+    gemm_pp_kernel<T, EPI, KFULL, SPLITK><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
+        p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base, splits, full, p.ws);
+}
 template <typename T, int EPI>
 static void launch_gemm_pp(const Args& p, int t_base, int blocks) {
-    using G = GemmCfg<MainCfg::WM, MainCfg::WN, MainCfg::FM, MainCfg::FN, MainCfg::KB, MainCfg::NS>;
-    if (p.K % MainCfg::KB == 0) {
-        const void* kern = reinterpret_cast<const void*>(&gemm_pp_kernel<T, EPI, true>);
-        static const hipError_t attr =
-            hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-        (void)attr;
-        gemm_pp_kernel<T, EPI, true><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
-            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
-    } else {
-        const void* kern = reinterpret_cast<const void*>(&gemm_pp_kernel<T, EPI, false>);
-        static const hipError_t attr =
-            hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-        (void)attr;
-        gemm_pp_kernel<T, EPI, false><<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
-            p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
-    }
+    if (p.K % MainCfg::KB == 0) launch_gemm_pp_k<T, EPI, true, false>(p, t_base, blocks, 1, 0);
+    else launch_gemm_pp_k<T, EPI, false, false>(p, t_base, blocks, 1, 0);
+}
+// `full` whole tiles from t_base, then `rem` tiles as `splits` K pieces each, in one launch
+template <typename T, int EPI>
+static void launch_gemm_pp_split(const Args& p, int t_base, int full, int rem, int splits) {
+    const int blocks = full + rem * splits;
+    if (p.K % MainCfg::KB == 0) launch_gemm_pp_k<T, EPI, true, true>(p, t_base, blocks, splits, full);
+    else launch_gemm_pp_k<T, EPI, false, true>(p, t_base, blocks, splits, full);
 }
 
 template <typename T, int EPI, typename C>
@@ -1541,8 +1612,43 @@ static void launch_stream_rows(const Args& p) {
     }
 }
 
+// The K-split remainder.  After the whole rounds of super tiles over the CUs, a last partial round of rem <= CUs / 2
+// tiles leaves most CUs idle or, as quarter tiles, runs at a lower MFMA rate; instead each of those tiles runs as
+// `splits` K pieces on the main configuration (rem * splits <= CUs workgroups), pieces of at least SPLIT_MIN_STAGES
+// 128-byte stages, their int32 partial sums met in a workspace.  Returns the splits for M x N x K under the default
+// policy (1: no split) and the workspace bytes it needs.
+constexpr int SPLIT_MIN_STAGES = 4, SPLIT_MAX = 8;
+static bool gemm_mid_path(int M, int N) {
+    return mid_stream(M, N) || M <= MID_GEMM_MAX_M || (M <= 2 * MID_GEMM_MAX_M && N <= 8192);
+}
+static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* bytes) {
+    const int tiles = ((M + SUPER - 1) / SUPER) * ((N + SUPER - 1) / SUPER);
+    *full = tiles / cus * cus;
+    *rem = tiles - *full;
+    *bytes = 0;
+    if (gemm_mid_path(M, N) || *rem == 0 || *rem > cus / 2 || *rem > SPLIT_HEAD_INTS) return 1;
+    const int nk = (K + 127) / 128;
+    const int s = min(min(cus / *rem, nk / SPLIT_MIN_STAGES), SPLIT_MAX);
+    if (s < 2) return 1;
+    *bytes = (long)SPLIT_HEAD_INTS * 4 + (long)*rem * s * SPLIT_SLOT_INTS * 4;
+    return s;
+}
+
 template <typename T, int EPI>
 static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
+    if (policy == 1 && p.ws) {                           // the K-split remainder, when the caller gave a workspace
+        int full, rem;
+        long bytes;
+        const int s = split_plan(p.M, p.N, p.K, cu_count(), &full, &rem, &bytes);
+        if (s >= 2 && bytes <= p.ws_bytes) {
+            // whole rounds before the last as their own launch; the last whole round and the pieces as one, so that
+            // the pieces start on each CU as its whole tile ends
+            const int cus = cu_count(), lead = full > cus ? full - cus : 0;
+            if (lead > 0) launch_gemm_pp<T, EPI>(p, 0, lead);
+            launch_gemm_pp_split<T, EPI>(p, lead, full - lead, rem, s);
+            return;
+        }
+    }
     if (policy == 1 && mid_stream(p.M, p.N)) {
         launch_stream_rows<T, EPI>(p);
         return;
@@ -1680,6 +1786,43 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
     const Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, out,
                  M, N, K, sa_rows, sw_rows, (hipStream_t)stream};
     if (M <= 32) {
+        if (bias) dispatch_dtype_stream<EPI_LARGE_BIAS>(p, dtype);
+        else dispatch_dtype_stream<EPI_LARGE>(p, dtype);
+    } else {
+        if (bias) dispatch_dtype_gemm<EPI_LARGE_BIAS>(p, dtype);
+        else dispatch_dtype_gemm<EPI_LARGE>(p, dtype);
+    }
+    return (int)hipGetLastError();
+}
+
+// Workspace bytes w8a8_scaled_mm_ws takes for M x N x K on the current device (0: that shape does not split); -1 on
+// bad sizes.
+extern "C" long w8a8_scaled_mm_ws_size(int M, int N, int K) {
+    if (M < 1 || N < 1 || K < 16) return -1;
+    int full, rem;
+    long bytes;
+    split_plan(M, N, K, cu_count(), &full, &rem, &bytes);
+    return bytes;
+}
+
+// w8a8_scaled_mm with a workspace (16-byte aligned, ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K); its first 4 KB zero
+// before the first call, and every call leaves them zero) for the K-split remainder of the prefill GEMM; dtype 2
+// writes the raw int32 accumulators to out [M, N] instead (sa, sw, bias unused).  Calls that share a workspace must
+// not overlap.  Returns -1 on bad arguments (a workspace too small included), else the HIP error of the launches.
+extern "C" int w8a8_scaled_mm_ws(const void* a, const void* w, const void* sa, const void* sw, const void* bias,
+                                 void* out, int M, int N, int K, int sa_rows, int sw_rows, int dtype, void* workspace,
+                                 long ws_bytes, void* stream) {
+    const bool raw = dtype == 2;
+    if (check_common(a, w, M, N, K, raw ? DT_F16 : dtype) != 0) return -1;
+    const long need = w8a8_scaled_mm_ws_size(M, N, K);
+    if (need > 0 && (!workspace || ws_bytes < need || ((uintptr_t)workspace & 15) != 0)) return -1;
+    Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, out, M, N,
+           K, sa_rows, sw_rows, (hipStream_t)stream};
+    p.ws = static_cast<int*>(workspace);
+    p.ws_bytes = ws_bytes;
+    if (raw) {
+        launch_gemm<f16, EPI_I32>(p);
+    } else if (M <= 32) {
         if (bias) dispatch_dtype_stream<EPI_LARGE_BIAS>(p, dtype);
         else dispatch_dtype_stream<EPI_LARGE>(p, dtype);
     } else {

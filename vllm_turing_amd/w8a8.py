@@ -9,10 +9,12 @@ is concrete):
     v_dot4 VALU kernel at one or two rows, else the LDS-ring int8 MFMA kernel)
   * M <= VLLM_TURING_MMA_MAX_M (default and maximum 32) -> w8a8_mma    (the MFMA kernel, two 16-row activation tiles
     past 16 rows)
-  * M > MMA_MAX_M, no bias, per-row / per-column scales -> w8a8_big    (prefill MFMA GEMM, large-M epilogue)
+  * M > MMA_MAX_M, no bias, per-row / per-column scales -> w8a8_big's prefill MFMA GEMM (large-M epilogue)
   * anything else                                       -> w8a8_scaled_mm (prefill or streaming kernel with the
     large-M epilogue of vLLM's cutlass_scaled_mm, with bias / per-tensor scales; the reference sends these to vLLM's
     CUTLASS op, w8a8.py:117, or to triton_scaled_mm for non-16-multiple shapes, w8a8.py:141-143)
+The last two run through w8a8_scaled_mm_ws with a per-device, per-stream workspace (workspace()), so that a last
+partial round of 256 x 256 tiles runs split over K; the results are bit-identical to the entries without it.
 The predicates gemv_ok / mma_ok / big_ok keep the reference's layout requirements (w8a8.py:38-46,58-66,78-79).
 Operands that fail them are made conforming (contiguous copies, zero padding of K to a multiple of 16) for the
 general kernel.  Every path runs a HIP kernel; there is no torch fallback.
@@ -89,11 +91,45 @@ def mma(out, a, b, sa, sb, bias):
                           _lib.stream_handle(a.device)), "w8a8_mma launch")
 
 
+_WS = {}
+
+
+def workspace(M, N, K, device):
+    """The K-split workspace w8a8_scaled_mm_ws takes for M x N x K on `device`'s current stream (one per device and
+    stream, zeroed once, sized for the largest split plan), or None: when the shape does not split, or when the stream
+    has none yet and is capturing a graph (a zero fill recorded there would run only at replay)."""
+    need = lib().w8a8_scaled_mm_ws_size(M, N, K)
+    if need <= 0:
+        return None
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        ws = torch.zeros(max(need, 4096 + cus * 262144), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def _scaled_mm_ws(a_ptr, w_ptr, sa, sb, bias, out, M, N, K, device, name):
+    """The large-M-epilogue entry, with the K-split workspace where the shape has one."""
+    ws = workspace(M, N, K, device)
+    args = (a_ptr, w_ptr, sa.data_ptr(), sb.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, int(sa.numel() > 1),
+            int(sb.numel() > 1), _lib.dtype_code(out.dtype))
+    if ws is None:
+        _check(lib().w8a8_scaled_mm(*args, _lib.stream_handle(device)), name)
+    else:
+        _check(lib().w8a8_scaled_mm_ws(*args, ws.data_ptr(), ws.numel(), _lib.stream_handle(device)), name)
+
+
 def big(out, a, b, sa, sb):
+    """The prefill path of w8a8_big (vllm_turing/w8a8.py:92-101): the same kernels and large-M epilogue, through the
+    workspace entry so that a last partial round of tiles runs split over K."""
     M, K = a.shape
     N = b.shape[1]
-    _check(lib().w8a8_big(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), out.data_ptr(), M, N, K,
-                          _lib.dtype_code(out.dtype), _lib.stream_handle(a.device)), "w8a8_big")
+    _scaled_mm_ws(a.data_ptr(), b.data_ptr(), sa, sb, None, out, M, N, K, a.device, "w8a8_big")
 
 
 def general(out, a, b, sa, sb, bias):
@@ -120,9 +156,7 @@ def general(out, a, b, sa, sb, bias):
     if bias is not None:
         bias = bias.to(out.dtype).contiguous().reshape(-1)
     dst = out if out.is_contiguous() else torch.empty((M, N), dtype=out.dtype, device=out.device)
-    _check(lib().w8a8_scaled_mm(a.data_ptr(), w.data_ptr(), sa.data_ptr(), sb.data_ptr(), _ptr(bias), dst.data_ptr(),
-                                M, N, K, int(sa.numel() > 1), int(sb.numel() > 1), _lib.dtype_code(out.dtype),
-                                _lib.stream_handle(a.device)), "w8a8_scaled_mm launch")
+    _scaled_mm_ws(a.data_ptr(), w.data_ptr(), sa, sb, bias, dst, M, N, K, a.device, "w8a8_scaled_mm launch")
     if dst is not out:
         out.copy_(dst)
 
