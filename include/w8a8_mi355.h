@@ -2,9 +2,10 @@
  * C ABI of the MI355X (gfx950) W8A8 SmoothQuant linear path: libw8a8_mi355.so.
  *
  * Plain pointers and sizes only.  Every buffer is allocated by the caller (torch tensors on the Python side); no entry
- * point allocates, synchronizes or keeps state, so every launch is asynchronous on `stream` (a hipStream_t, e.g.
- * torch.cuda.current_stream().cuda_stream) and can be captured in a HIP graph.  Argument validation happens before any
- * HIP call and returns the documented code.
+ * point allocates or synchronizes, so every launch is asynchronous on `stream` (a hipStream_t, e.g.
+ * torch.cuda.current_stream().cuda_stream) and can be captured in a HIP graph.  None keeps state, except in the
+ * workspace a caller passes to w8a8_scaled_mm_ws and in the per-GPU scratch of w8a8_scaled_mm_noalloc (tile counters
+ * that every call leaves at zero).  Argument validation happens before any HIP call and returns the documented code.
  *
  * dtype: 0 = float16, 1 = bfloat16 (activations, bias and output).  Weights are int8 [N, K] row-major (the layout vLLM
  * stores; its cutlass_scaled_mm receives the [K, N] stride-(1, K) view of it).  Scales are float32: sa [M] (sa_rows=1)
@@ -70,6 +71,16 @@ int w8a8_scaled_mm_ws(const void* a, const void* w, const void* sa, const void* 
 /* Workspace bytes w8a8_scaled_mm_ws takes for M x N x K on the current device: 0 when the shape does not split, at
  * most 4 KB + 256 KB per CU; -1 for M, N < 1 or K < 16. */
 long w8a8_scaled_mm_ws_size(int M, int N, int K);
+
+/* w8a8_scaled_mm_ws that allocates nothing: the same arguments without the workspace, whose place the library's own
+ * scratch takes (a static device array of 64 MiB + 4 KiB per GPU, held until the process ends; its address is looked
+ * up once per device).  No counterpart in the reference: for callers that cannot allocate (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc).  Every call on a GPU shares that GPU's scratch, so
+ * calls that overlap on one GPU (other streams or threads) race.  Returns -1 on bad arguments, -2 when the shape's K
+ * split needs more than the scratch holds (more than 256 CUs), -3 when the scratch's address cannot be had, else the
+ * HIP error code of the launches. */
+int w8a8_scaled_mm_noalloc(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* out,
+                           int M, int N, int K, int sa_rows, int sw_rows, int dtype, void* stream);
 
 /* Dynamic symmetric per-token int8 quantization: scales[m] = absmax_m / 127,
  * q[m, k] = clamp(rint(float(x[m, k]) * (127 / absmax_m)), -128, 127); a zero row gives q = 0 and scale 0.

@@ -69,6 +69,11 @@ def test_argument_validation_codes(L):
     assert L.w8a8_scaled_mm_ws_size(200, 1024, 5120) == 0       # a mid-M shape: no split
     assert L.w8a8_scaled_mm_ws_size(4096, 12288, 5120) == 0     # 768 super tiles: whole rounds on 256 CUs
     assert L.w8a8_scaled_mm_ws_size(512, 12288, 512) == 0       # 4 K stages: pieces would be under 4 stages
+    # w8a8_scaled_mm_noalloc: the same validation, before any HIP call
+    assert L.w8a8_scaled_mm_noalloc(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
+    assert L.w8a8_scaled_mm_noalloc(16, 16, 0, 0, None, 0, 64, 64, 40, 1, 1, 0, None) == -1   # K % 16
+    assert L.w8a8_scaled_mm_noalloc(17, 16, 0, 0, None, 0, 64, 64, 64, 1, 1, 0, None) == -1   # misaligned a
+    assert L.w8a8_scaled_mm_noalloc(16, 16, 0, 0, None, 0, 64, 64, 64, 1, 1, 3, None) == -1   # dtype 0..2
     assert L.w8a8_i32(16, 16, 0, 65, 64, 64, 0, None) == -1                       # streaming kernel: M <= 64
     assert L.w8a8_i32(16, 16, 0, 6, 64, 64, 2, None) == -1                       # VALU kernel: M <= 5
     assert L.w8a8_i32(16, 16, 0, 1, 64, 17424, 2, None) == -1                    # K <= 17408 at one row

@@ -1832,6 +1832,64 @@ extern "C" int w8a8_scaled_mm_ws(const void* a, const void* w, const void* sa, c
     return (int)hipGetLastError();
 }
 
+// ---- w8a8_scaled_mm_noalloc: w8a8_scaled_mm_ws with the library's own scratch in place of the workspace ------------
+// For callers that cannot allocate (HIP graph capture, serving loops that forbid allocation).  The scratch is a
+// file-scope device array: 4 KB of tile counters and 256 accumulator slots of 256 KB (64 MiB + 4 KiB), enough for the
+// K split of any shape on a GPU of up to 256 CUs (a larger need is rejected).  Each GPU the library runs on holds its
+// own copy until the process ends; every call on a GPU shares it, so calls that overlap on one GPU (other streams,
+// other threads) race.  In host code `scratch` only names the host-side stand-in of the array: its device address
+// comes from hipGetSymbolAddress, once per device, and is what the kernels get.
+constexpr long NOALLOC_SLOTS = 256;
+constexpr long NOALLOC_SCRATCH_INTS = SPLIT_HEAD_INTS + NOALLOC_SLOTS * SPLIT_SLOT_INTS;
+static __device__ __align__(256) int scratch[NOALLOC_SCRATCH_INTS];
+
+__global__ void __launch_bounds__(256) clear_ints_kernel(int* __restrict__ p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
+// The device address of this device's scratch (null on failure).  The first call on a device also clears the tile
+// counters with a kernel on `st` (the loader's zero fill of the array is not relied on); a call under stream capture
+// records that clear in the graph (harmless: the counters are zero whenever no call runs) and leaves the eager clear
+// to the next call outside capture.
+static int* scratch_setup(hipStream_t st) {
+    constexpr int MAX_DEV = 64;
+    static std::atomic<int*> addr[MAX_DEV];
+    static std::atomic<bool> cleared[MAX_DEV];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return nullptr;
+    int* p = addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void* q = nullptr;
+        if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return nullptr;
+        p = static_cast<int*>(q);
+        addr[dev].store(p, std::memory_order_release);
+    }
+    if (!cleared[dev].load(std::memory_order_acquire)) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        const bool capturing = hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+        clear_ints_kernel<<<1, 256, 0, st>>>(p, SPLIT_HEAD_INTS);
+        if (hipGetLastError() != hipSuccess) return nullptr;
+        if (!capturing) cleared[dev].store(true, std::memory_order_release);
+    }
+    return p;
+}
+
+// w8a8_scaled_mm_ws's arguments without the workspace.  Returns -1 on bad arguments, -2 when the shape's K split
+// would need more than the scratch holds, -3 when the scratch's address cannot be had, else the HIP error of the
+// launches.  Allocates nothing.
+extern "C" int w8a8_scaled_mm_noalloc(const void* a, const void* w, const void* sa, const void* sw, const void* bias,
+                                      void* out, int M, int N, int K, int sa_rows, int sw_rows, int dtype,
+                                      void* stream) {
+    if (check_common(a, w, M, N, K, dtype == 2 ? DT_F16 : dtype) != 0) return -1;
+    const long need = w8a8_scaled_mm_ws_size(M, N, K);
+    if (need < 0) return -1;
+    if (need > NOALLOC_SCRATCH_INTS * 4) return -2;
+    int* ws = nullptr;
+    if (need > 0 && !(ws = scratch_setup((hipStream_t)stream))) return -3;
+    return w8a8_scaled_mm_ws(a, w, sa, sw, bias, out, M, N, K, sa_rows, sw_rows, dtype, ws,
+                             ws ? NOALLOC_SCRATCH_INTS * 4 : 0, stream);
+}
+
 // Test export: the raw int32 accumulators acc [M, N] of one kernel's main loop (kernel 0 = the MFMA streaming kernel,
 // M <= 64; kernel 1 = the prefill kernel as dispatched; kernel 2 = the VALU dot4 kernel, M = 1 and K <= 17408,
 // M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120; kernel 3 = the prefill kernel's quarter-tile configuration alone;
