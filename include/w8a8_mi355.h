@@ -56,7 +56,7 @@ int w8a8_scaled_mm(const void* a, const void* w, const void* sa, const void* sw,
 
 /* w8a8_scaled_mm (and so w8a8_big, which is its no-bias per-row / per-column case) with a caller workspace for the
  * prefill GEMM's K split: when the 256 x 256 super tiles leave a last partial round of at most half the CUs, each of
- * those tiles runs as 2..8 K pieces whose int32 partial sums meet in the workspace (the last piece to finish adds
+ * those tiles runs as 2..8 K pieces (at least 3 after whole rounds) whose int32 partial sums meet in the workspace (the last piece to finish adds
  * them and runs the epilogue; the results are bit-identical to w8a8_scaled_mm's).  workspace: 16-byte aligned,
  * ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K) (it may be null when that is 0); its first 4 KB (tile counters) must be
  * zero before the first call, and every call leaves them zero.  Calls that share a workspace must not overlap.

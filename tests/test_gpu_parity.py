@@ -705,13 +705,13 @@ def test_scaled_mm_bits(L, M, N, K, dt, with_bias, per_tensor, order):
 # the prefill GEMM's K split (w8a8_scaled_mm_ws): the last partial round of super tiles as K pieces met in a workspace
 # ---------------------------------------------------------------------------------------------------------------------
 SPLIT_SHAPES = [
-    (512, 12288, 5120),     # 96 super tiles x 2 pieces
-    (2048, 12288, 5120),    # 256 whole tiles, then 128 x 2
+    (512, 12288, 5120),     # 96 super tiles x 2 pieces of 20 stages
+    (1536, 14336, 17408),   # 256 whole tiles and 80 x 3 pieces in one launch
     (4096, 5120, 17408),    # 256 whole, then 64 x 4 (the MLP down projection)
-    (1000, 3000, 2064),     # 48 x 4, ragged M, N and K (K % 128 = 16: the last stage zero-filled)
-    (768, 8192, 1024),      # 96 x 2 at 8 stages
-    (300, 1000, 5120),      # 8 x 8
-    (4096, 17152, 2048),    # 1072 tiles: 768 whole in a launch of their own, 256 whole + 48 x 4 in the next
+    (1000, 3000, 17424),    # 48 x 5, ragged M, N and K (K % 128 = 16: the last stage zero-filled)
+    (768, 8192, 10240),     # 96 x 2 at 80 stages
+    (300, 1000, 17408),     # 8 x 8
+    (4096, 9472, 17408),    # 592 tiles: 256 whole in a launch of their own, 256 whole + 80 x 3 in the next
 ]
 
 
@@ -754,8 +754,8 @@ def test_split_i32(L, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K,dt,with_bias", [(512, 12288, 5120, torch.bfloat16, True),
-                                                (1000, 3000, 2064, torch.float16, False),
-                                                (2048, 12288, 5120, torch.float16, True)])
+                                                (1000, 3000, 17424, torch.float16, False),
+                                                (1536, 14336, 17408, torch.float16, True)])
 def test_split_bits(L, M, N, K, dt, with_bias):
     """16-bit outputs of the split path bit-identical to w8a8_scaled_mm's (no workspace) and to the oracle's large-M
     epilogue of the exact products."""
@@ -788,7 +788,7 @@ def test_split_shared_workspace_and_graph(L):
     """One workspace for calls of different shapes in a row, then the split path captured in a HIP graph and replayed
     three times with eager work in between: every result equal to the eager one."""
     say("split shared workspace + graph replay")
-    shapes = [(1000, 3000, 2064), (300, 1000, 5120), (1000, 3000, 2064)]
+    shapes = [(1000, 3000, 17424), (300, 1000, 17408), (1000, 3000, 17424)]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     ws = torch.zeros(4096 + cus * 262144, dtype=torch.uint8, device=DEV)
     g = torch.Generator().manual_seed(5)
@@ -796,7 +796,7 @@ def test_split_shared_workspace_and_graph(L):
     for M, N, K in shapes:
         a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
         w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
-        ref = torch.from_numpy(oracle.gemm_i32(a.numpy(), w.numpy()))
+        ref = torch._int_mm(a, w.t())
         ops.append((a.to(DEV), w.to(DEV), torch.empty(M, N, dtype=torch.int32, device=DEV), ref))
     for a, w, acc, ref in ops:
         ws_call(L, a, w, None, None, None, acc, ws, 2)

@@ -25,9 +25,9 @@ def bits(t):
 def test_noalloc_matches_workspace_entry(L):
     st = torch.cuda.current_stream().cuda_stream
     g = torch.Generator().manual_seed(11)
-    # two calls in a row, the second with a smaller input; both split over K (M=2048: 256 whole tiles + 128 x 2 pieces;
-    # M=512: 96 x 2 pieces)
-    for M, N, K in ((2048, 12288, 5120), (512, 12288, 5120)):
+    # two calls in a row, the second with a smaller input; both split over K (M=4096, N=5120, K=17408: 256 whole tiles
+    # + 64 x 4 pieces, every slot of the scratch; M=512: 96 x 2 pieces)
+    for M, N, K in ((4096, 5120, 17408), (512, 12288, 5120)):
         print(f"noalloc M={M} N={N} K={K}", flush=True)
         need = L.w8a8_scaled_mm_ws_size(M, N, K)
         assert need > 4096

@@ -1615,9 +1615,15 @@ static void launch_stream_rows(const Args& p) {
 // The K-split remainder.  After the whole rounds of super tiles over the CUs, a last partial round of rem <= CUs / 2
 // tiles leaves most CUs idle or, as quarter tiles, runs at a lower MFMA rate; instead each of those tiles runs as
 // `splits` K pieces on the main configuration (rem * splits <= CUs workgroups), pieces of at least SPLIT_MIN_STAGES
-// 128-byte stages, their int32 partial sums met in a workspace.  Returns the splits for M x N x K under the default
-// policy (1: no split) and the workspace bytes it needs.
-constexpr int SPLIT_MIN_STAGES = 4, SPLIT_MAX = 8;
+// 128-byte stages, their int32 partial sums met in a workspace.  Same box, rotated weights, against the quarter
+// tiles: M 512 x N 12288 x K 5120 (96 x 2) 55.3 -> 44.8 us, M 1024 x N 5120 x K 17408 (80 x 3) 123.8 -> 93.1 us,
+// M 4096 x N 5120 x K 17408 (256 whole + 64 x 4) 313.8 -> 299.4 us.  Returns the splits for M x N x K under the
+// default policy (1: no split) and the workspace bytes it needs.
+// Pieces of at least 16 stages: shorter ones are dominated by a piece's fixed cost (prologue, partial exchange,
+// epilogue: ~15 us against ~1.45 us per stage) and lose to, or tie with, the 4-stage quarter tiles (same box: M 512
+// x N 34816 x K 5120, 256 whole + 16 tiles as 16 x 8 pieces of 5 stages 111.0 us against 104.9, as 16 x 4 of 10
+// stages 103.7 against 105.0; M 4096 x N 17152 x K 5120, 48 x 4 of 10 stages 323.7 against 310.2).
+constexpr int SPLIT_MIN_STAGES = 16, SPLIT_MAX = 8;
 static bool gemm_mid_path(int M, int N) {
     return mid_stream(M, N) || M <= MID_GEMM_MAX_M || (M <= 2 * MID_GEMM_MAX_M && N <= 8192);
 }
@@ -1629,7 +1635,19 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
     if (gemm_mid_path(M, N) || *rem == 0 || *rem > cus / 2 || *rem > SPLIT_HEAD_INTS) return 1;
     const int nk = (K + 127) / 128;
     const int s = min(min(cus / *rem, nk / SPLIT_MIN_STAGES), SPLIT_MAX);
-    if (s < 2) return 1;
+    // two pieces after whole rounds lose to the quarter tiles (same box, rotated weights: M 2048 x N 12288 x K 5120
+    // 118.1 -> 123.7 us, M 8192 x N 5120 x K 5120 184.5 -> 192.0): the pieces of the whole round's CUs all finish
+    // together and write their partials in one burst, where 512 quarter tiles run two per CU
+    if (s < 2 || (s == 2 && *full > 0)) return 1;
+    // after whole rounds, pieces shorter than 32 stages tie or lose (same box: M 4096 x N 9472 x K 6144, 80 x 3 of 16
+    // stages, 222.4 us against 215.8; M 1536 x N 14336 x K 6144 135.8 against 134.7); the MLP down projection's 64 x 4
+    // of 34 stages wins (313.8 -> 299.4 us)
+    if (*full > 0 && nk / s < 32) return 1;
+    // where the quarter tiles run one per CU with 4 stages (4 rem <= CUs) they take ~0.42 of a whole tile's time
+    // (~nk + 8 stages); a piece takes nk / s stages plus ~8 stages of fixed cost.  Same box: M 1000 x N 3000 x
+    // K 4112 (48 x 2) 24.7 us as quarter tiles against 31.9 split; M 4096 x N 17152 x K 6144 (48 x 3 after whole
+    // rounds) 353.1 against 359.4; M 300 x N 1000 x K 17408 (8 x 8) 76.8 against 44.9
+    if (4 * *rem <= cus && 100 * (nk / s + 8) >= 42 * (nk + 8)) return 1;
     *bytes = (long)SPLIT_HEAD_INTS * 4 + (long)*rem * s * SPLIT_SLOT_INTS * 4;
     return s;
 }
