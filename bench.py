@@ -363,7 +363,9 @@ def bench_stack(torch, L, st, dev, ms_list=(1, 4, 4096)):
     res = {"workload": f"64-layer linear stack, {len(shapes)} projections, {n_params / 1e9:.2f} G int8 weights, "
                        f"bf16 activations; per layer residual add + RMSNorm + quant -> mixer in -> quant -> mixer out "
                        f"-> residual add + RMSNorm + quant -> gate_up -> SiLU*up+quant -> down; at M <= 12 the mixer "
-                       f"out-projection quantizes its input inside the GEMV (w8a8_gemv_quant)", "passes": {}}
+                       f"out-projection quantizes its input inside the GEMV (w8a8_gemv_quant); at M <= 5 the MLP runs "
+                       f"as the package's decode MLP: SiLU*up in the gate_up GEMV (w8a8_gemv_silu), the down GEMV "
+                       f"quantizing its input (w8a8_gemv_quant)", "passes": {}}
     for M in ms_list:
         kmax = max(K for (_, _, _, K) in shapes)
         nmax = max(N for (_, _, N, _) in shapes)
@@ -376,9 +378,24 @@ def bench_stack(torch, L, st, dev, ms_list=(1, 4, 4096)):
         o = torch.empty(M * nmax, dtype=torch.bfloat16, device=dev)
         d = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
 
+        fused_mlp = M <= 5                                    # the package's decode MLP (tailoverlap.mlp_quantized)
+
         def one_pass(i=0):
             for li, (_, name, N, K) in enumerate(shapes):
                 w, sw = weights[li]
+                if name == "gate_up" and fused_mlp:               # SiLU * up in the gate_up GEMV's epilogue
+                    if L.rms_norm_quant(x.data_ptr(), resid.data_ptr(), nw.data_ptr(), None, 1e-6, q.data_ptr(),
+                                        s.data_ptr(), M, K, 1, st()) != 0:
+                        raise RuntimeError("rms_norm_quant")
+                    if L.w8a8_gemv_silu(q.data_ptr(), w.data_ptr(), s.data_ptr(), sw.data_ptr(), None, o.data_ptr(),
+                                        M, I, K, 1, 1, 1, st()) != 0:
+                        raise RuntimeError("w8a8_gemv_silu")
+                    continue
+                if name == "down" and fused_mlp:                  # the down GEMV quantizes silu(g) * u itself
+                    if L.w8a8_gemv_quant(o.data_ptr(), I, q.data_ptr(), s.data_ptr(), w.data_ptr(), sw.data_ptr(),
+                                         None, d.data_ptr(), M, N, K, 1, 1, st()) != 0:
+                        raise RuntimeError("w8a8_gemv_quant")
+                    continue
                 if name == "down":
                     src = o[:M * 2 * I].view(M, 2 * I)          # the gate_up output of this layer
                     if L.silu_mul_quant_bf16(src.data_ptr(), q.data_ptr(), s.data_ptr(), M, I, st()) != 0:

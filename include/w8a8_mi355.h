@@ -40,6 +40,17 @@ int w8a8_mma(const void* a, const void* w, const void* sa, const void* sw, const
 int w8a8_gemv_quant(const void* x, long ldx, void* xq, void* xs, const void* w, const void* sw, const void* bias,
                     void* out, int M, int N, int K, int sw_rows, int dtype, void* stream);
 
+/* The decode MLP's gate_up GEMV with SiLU * up in its epilogue: a [M, K] int8, w [2I, K] int8 (gate rows 0..I-1, up
+ * rows I..2I-1), sa [M] or [1], sw [2I] or [1], bias [2I] of the output type or null; h [M, I] = T(float(silu_h(g)) *
+ * float(u)) where g = out[m, p] and u = out[m, p + I] are the outputs w8a8_gemv would write (small-M epilogue) and
+ * silu_h is silu_mul_quant's 16-bit silu, so per_token_quant(h) equals silu_mul_quant(w8a8_gemv output) bit for bit.
+ * Taken where the VALU GEMV takes M and K (M <= 5; K <= 17408 at one row, 8192 at two or three, 5120 at four or
+ * five).  No counterpart in the reference, whose MLP runs the GEMV and silu_quant.cu:71 as two launches
+ * (vllm_turing/tailoverlap.py:146-151).  Returns -1 on bad arguments, 1 for M or K outside that range, else the HIP
+ * launch error. */
+int w8a8_gemv_silu(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* h, int M,
+                   int I, int K, int sa_rows, int sw_rows, int dtype, void* stream);
+
 /* Prefill W8A8 GEMM, any M (dispatched for M > 32), per-row sa [M] and per-column sw [N], no bias, N % 16 == 0:
  * out[m, n] = T(sa[m] * float(float(acc) * sw[n])).
  * Replaces vllm_turing/csrc/w8a8_big.cu:66 (same arguments).  Returns 0 ok, 1 cannot implement (shape, alignment),

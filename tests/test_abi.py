@@ -69,6 +69,12 @@ def test_argument_validation_codes(L):
     assert L.w8a8_scaled_mm_ws_size(200, 1024, 5120) == 0       # a mid-M shape: no split
     assert L.w8a8_scaled_mm_ws_size(4096, 12288, 5120) == 0     # 768 super tiles: whole rounds on 256 CUs
     assert L.w8a8_scaled_mm_ws_size(512, 12288, 512) == 0       # 4 K stages: pieces would be under 4 stages
+    # w8a8_gemv_silu: -1 on bad arguments, 1 where the VALU GEMV does not take M or K
+    assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 0, 5120, 1, 1, 0, None) == -1      # I < 1
+    assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 64, 40, 1, 1, 0, None) == -1      # K % 16
+    assert L.w8a8_gemv_silu(16, 16, 0, 0, None, None, 1, 64, 64, 1, 1, 0, None) == -1    # no output
+    assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 6, 64, 64, 1, 1, 0, None) == 1       # M = 6: not the VALU GEMV
+    assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 4, 64, 8192, 1, 1, 0, None) == 1     # K past four rows' limit
     # w8a8_scaled_mm_noalloc: the same validation, before any HIP call
     assert L.w8a8_scaled_mm_noalloc(16, 16, 0, 0, None, 0, 0, 64, 64, 1, 1, 0, None) == -1
     assert L.w8a8_scaled_mm_noalloc(16, 16, 0, 0, None, 0, 64, 64, 40, 1, 1, 0, None) == -1   # K % 16

@@ -881,6 +881,71 @@ def test_gemv_quant_bits(L, M, N, K, dt, extra, with_bias, zero_row):
         assert torch.equal(y, out)
 
 
+GEMV_SILU_CASES = [
+    # M, I, K, dtype, bias, per-tensor scales
+    (1, 17408, 5120, torch.bfloat16, False, False),      # the decode gate_up of the stack at one row
+    (1, 2000, 17408, torch.float16, True, False),        # the longest K at one row
+    (2, 1000, 8192, torch.float16, False, True),         # per-tensor activation scale
+    (3, 333, 5136, torch.bfloat16, True, False),         # K not a multiple of the 1 KB row chunk
+    (4, 17408, 5120, torch.float16, False, False),
+    (5, 64, 16, torch.bfloat16, True, True),
+    (1, 7, 5120, torch.float16, False, False),           # fewer pairs than lanes of one wavefront
+]
+
+
+@pytest.mark.parametrize("M,I,K,dt,with_bias,per_tensor", GEMV_SILU_CASES)
+def test_gemv_silu_bits(L, M, I, K, dt, with_bias, per_tensor):
+    """w8a8_gemv_silu (SiLU * up in the gate_up GEMV's epilogue) against the oracle: the 16-bit silu(g) * u of the
+    oracle's gate_up output bit for bit, and per_token_quant of it equal to the oracle's silu_mul_quant (q and scales),
+    i.e. to silu_mul_quant of the GEMV's output; the package's decode MLP equal to its two-GEMM chain."""
+    say(f"gemv_silu M={M} I={I} K={K} {dt} bias={with_bias} per_tensor={per_tensor}")
+    g = torch.Generator().manual_seed(M * 5 + I + K)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    w = torch.randint(-128, 128, (2 * I, K), dtype=torch.int8, generator=g)
+    sa = torch.rand(1 if per_tensor else M, generator=g) * 1e-2 + 1e-4
+    sw = torch.rand(1 if per_tensor else 2 * I, generator=g) * 2e-3 + 1e-5
+    bias = torch.randn(2 * I, generator=g).to(dt) if with_bias else None
+    ad, wd, sad, swd = a.to(DEV), w.to(DEV), sa.to(DEV), sw.to(DEV)
+    bd = None if bias is None else bias.to(DEV)
+    h = torch.empty(M, I, dtype=dt, device=DEV)
+    assert L.w8a8_gemv_silu(ad.data_ptr(), wd.data_ptr(), sad.data_ptr(), swd.data_ptr(),
+                            None if bd is None else bd.data_ptr(), h.data_ptr(), M, I, K, int(not per_tensor),
+                            int(not per_tensor), code(dt), stream()) == 0
+    q = torch.empty(M, I, dtype=torch.int8, device=DEV)
+    s = torch.empty(M, dtype=torch.float32, device=DEV)
+    assert L.per_token_quant(h.data_ptr(), q.data_ptr(), s.data_ptr(), M, I, I, code(dt), stream()) == 0
+    torch.cuda.synchronize()
+    gu_bits = oracle.epilogue(oracle.gemm_i32(a.numpy(), w.numpy()), sa.numpy(), sw.numpy(),
+                              None if bias is None else bits(bias), code(dt), oracle.ORDER_SMALL_M)
+    gu = torch.from_numpy(gu_bits.view(np.int16)).view(dt)
+    qr, sr, act = oracle.silu_mul_quant(gu)
+    assert np.array_equal(bits(h), act), f"{int((bits(h) != act).sum())} of {act.size} silu * up values differ"
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_decode_mlp_fused_chain(L, M):
+    """mlp_quantized at decode row counts (gemv_silu, then the down GEMV quantizing its own input) against the
+    reference's chain through the dispatch (GEMV -> silu_mul_quant -> GEMV): identical outputs."""
+    say(f"decode MLP fused chain M={M}")
+    from vllm_turing_amd import tailoverlap, w8a8
+    H, I = 1024, 2048
+    g = torch.Generator().manual_seed(M)
+    x_q = torch.randint(-128, 128, (M, H), dtype=torch.int8, generator=g).to(DEV)
+    x_s = (torch.rand(M, 1, generator=g) * 1e-2 + 1e-4).to(DEV)
+    w_gu = torch.randint(-128, 128, (2 * I, H), dtype=torch.int8, generator=g).to(DEV)
+    sw_gu = (torch.rand(2 * I, 1, generator=g) * 2e-3 + 1e-5).to(DEV)
+    w_d = torch.randint(-128, 128, (H, I), dtype=torch.int8, generator=g).to(DEV)
+    sw_d = (torch.rand(H, 1, generator=g) * 2e-3 + 1e-5).to(DEV)
+    assert tailoverlap.gemv_silu_ok(x_q, x_s, w_gu, sw_gu)
+    got = tailoverlap.mlp_quantized(x_q, x_s, w_gu, sw_gu, w_d, sw_d, torch.bfloat16)
+    gate_up = w8a8.cutlass_scaled_mm(x_q, w_gu.t(), x_s, sw_gu, torch.bfloat16)
+    a_q, a_s = tailoverlap.silu_mul_quant(gate_up)
+    want = w8a8.cutlass_scaled_mm(a_q, w_d.t(), a_s, sw_d, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_dispatch_paths(L):
     from vllm_turing_amd import w8a8
     K, N = 5120, 1024

@@ -18,6 +18,7 @@ SIGNATURES = {
     "w8a8_scaled_mm_ws_size": [_i] * 3,
     "w8a8_scaled_mm_noalloc": [_vp] * 6 + [_i] * 6 + [_vp],
     "w8a8_gemv_quant": [_vp, _l, _vp, _vp] + [_vp] * 4 + [_i] * 5 + [_vp],
+    "w8a8_gemv_silu": [_vp] * 6 + [_i] * 6 + [_vp],
     "per_token_quant": [_vp] * 3 + [_i, _i, _l, _i, _vp],
     "silu_mul_quant": [_vp] * 3 + [_i] * 2 + [_vp],
     "silu_mul_quant_bf16": [_vp] * 3 + [_i] * 2 + [_vp],

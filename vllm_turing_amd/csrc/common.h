@@ -134,4 +134,18 @@ __device__ __forceinline__ int wave_sum(int v) {
     return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
 }
 
+// ---- SiLU(gate) * up in 16 bits (silu_quant.cu:11-14,39) ------------------------------------------------------------
+// silu rounded to the 16-bit type, then its exact float32 product with u (both 16-bit values) rounded once more.
+__device__ __forceinline__ float silu_f(float f) {
+    const float e = expf(-f);                               // HIP's float32 exp (within 2 float32 ulps here)
+    const float d = 1.0f + e;
+    return f / d;                                           // IEEE division
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t silu_mul(float g, float u) {
+    const uint16_t sh = from_float<T>(silu_f(g));
+    return from_float<T>(to_float(T{sh}) * u);            // exact float product of two 16-bit values, one rounding
+}
+
 }  // namespace w8

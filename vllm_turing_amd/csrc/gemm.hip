@@ -106,7 +106,11 @@ __device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sa
 // = absmax / 127; q = clamp(rint(x * (127 / absmax)))), while its wavefronts' first weight rows are already being
 // loaded (each workgroup reads the row once: per wavefront it cost ~140 MB of L2 reads at N = 5120); workgroup 0 also
 // writes the int8 rows to xq and the scales to xs.
-template <typename T, int M, int CH, int R, int EPI, bool NT = true, bool QX = false>
+// SILU: the weights are a gate_up projection of 2N rows (gate rows 0..N-1, up rows N..2N-1) and a row group is the
+// pair (p, p + N) (R = 2); instead of the two outputs the kernel writes out[m, p] = silu(g) * u in 16 bits, with g and
+// u rounded as the GEMV writes them and the product as silu_mul_quant forms it before quantizing
+// (vllm_turing/csrc/silu_quant.cu:39), so the decode MLP needs no separate SiLU kernel.
+template <typename T, int M, int CH, int R, int EPI, bool NT = true, bool QX = false, bool SILU = false>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
                                                         const uint16_t* __restrict__ bias, void* __restrict__ out,
@@ -118,6 +122,7 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
     const int nw = gridDim.x * (blockDim.x >> 6);
     const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int K16 = K >> 4;
+    static_assert(!SILU || (R == 2 && EPI == EPI_SMALL && !QX), "gate and up rows of one pair, small-M epilogue");
     const v4i z = {0, 0, 0, 0};
     v4i av[M][CH];
     float sam[M];                                        // row scales (none are read for the int32 output)
@@ -127,7 +132,7 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
     auto load = [&](int buf, int n0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = min(n0 + r * nw, N - 1);
+            const int n = SILU ? min(n0, N - 1) + r * N : min(n0 + r * nw, N - 1);
             const int8_t* row = w + (long)n * K;
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
@@ -159,6 +164,18 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
                 }
                 acc[r][m] = wave_sum(s);
             }
+        if constexpr (SILU) {                            // lane m writes out[m, n0]
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+                if (lane == m && n0 < N) {
+                    const float g = to_float(T{from_float<T>(epi_small(acc[0][m], sam[m], swb[buf][0],
+                                                                      to_float(T{bb[buf][0]})))});
+                    const float u = to_float(T{from_float<T>(epi_small(acc[1][m], sam[m], swb[buf][1],
+                                                                      to_float(T{bb[buf][1]})))});
+                    static_cast<uint16_t*>(out)[(long)m * N + n0] = silu_mul<T>(g, u);
+                }
+            return;
+        }
         // lane r * M + m writes output (m, n0 + r * nw)
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -172,7 +189,7 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
     // Row groups wid, wid + stride, ... (cnt of them), each computed while the next group's loads are in flight.  The
     // loop is peeled so that no load sits under a condition: then the compiler's wait before a group's math counts
     // the next group's loads as still outstanding instead of waiting for them too.
-    const int stride = R * nw;
+    const int stride = SILU ? nw : R * nw;
     if constexpr (!QX) {
         if (wid >= N) return;
     }
@@ -1362,7 +1379,10 @@ static void launch_dot4_ch(const Args& p) {
                     nb = 1;
                 return nb < DOT4_BLOCKS_PER_CU ? nb : DOT4_BLOCKS_PER_CU;
             }();
-            const int need = (p.N + 3) / 4, grid = cu_count() * per_cu;
+            // three rows per wavefront, as the plain kernel's one-row grid: every workgroup quantizes the row again,
+            // so fewer, fuller workgroups (one row per wavefront: K = 6144, N = 5120 9.07 -> 8.55 us; K = 17408
+            // 18.83 -> 18.62 us; two rows per wavefront no better)
+            const int need = (p.N + 11) / 12, grid = cu_count() * per_cu;
             kern<<<need < grid ? need : grid, 256, p.M * p.K + 64, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N,
                                                                           p.K, p.sa_rows, p.sw_rows, p.x, p.ldx,
                                                                           p.xq, p.xs);
@@ -1391,6 +1411,43 @@ static void launch_dot4_m(const Args& p) {
         }
     }
 }
+// gate_up with SiLU * up (SILU above): p.N pairs; at M <= 2 one wavefront per workgroup with two pairs (four rows)
+// each, else the grid of the plain kernel.
+template <typename T, int M, int CH>
+static void launch_dot4_silu_ch(const Args& p) {
+    if constexpr (CH <= DOT4_MAX_CH && (M < 2 || CH <= DOT4_MAX_CH_M2) && (M < 4 || CH <= DOT4_MAX_CH_M4)) {
+        const auto kern = &gemv_dot4_kernel<T, M, CH, 2, EPI_SMALL, true, false, true>;
+        if constexpr (M <= 2) {
+            kern<<<(p.N + 1) / 2, 64, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows,
+                                                 nullptr, 0, nullptr, nullptr);
+            return;
+        }
+        static const int per_cu = row_stream_per_cu(reinterpret_cast<const void*>(kern));
+        const int need = (p.N + 3) / 4, grid = cu_count() * per_cu;
+        kern<<<need < grid ? need : grid, 256, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows,
+                                                          p.sw_rows, nullptr, 0, nullptr, nullptr);
+    }
+}
+template <typename T, int M>
+static void launch_dot4_silu_m(const Args& p) {
+    switch (dot4_chunks(p.K)) {
+#define W8_CASE(C) case C: launch_dot4_silu_ch<T, M, C>(p); break;
+        W8_CASE(1) W8_CASE(2) W8_CASE(3) W8_CASE(4) W8_CASE(5) W8_CASE(6) W8_CASE(7) W8_CASE(8) W8_CASE(10)
+        W8_CASE(12) W8_CASE(14) W8_CASE(17)
+#undef W8_CASE
+    }
+}
+template <typename T>
+static void launch_dot4_silu(const Args& p) {
+    switch (p.M) {
+        case 1: launch_dot4_silu_m<T, 1>(p); break;
+        case 2: launch_dot4_silu_m<T, 2>(p); break;
+        case 3: launch_dot4_silu_m<T, 3>(p); break;
+        case 4: launch_dot4_silu_m<T, 4>(p); break;
+        case 5: launch_dot4_silu_m<T, 5>(p); break;
+    }
+}
+
 static bool dot4_ok(const Args& p) {
     return p.M <= DOT4_MAX_M &&
            dot4_chunks(p.K) <= (p.M < 2 ? DOT4_MAX_CH : p.M < 4 ? DOT4_MAX_CH_M2 : DOT4_MAX_CH_M4);
@@ -1780,6 +1837,22 @@ extern "C" int w8a8_gemv_quant(const void* x, long ldx, void* xq, void* xs, cons
     const int rc = per_token_quant(x, xq, xs, M, K, ldx, dtype, stream);
     if (rc != 0) return rc;
     dispatch_dtype_stream<EPI_SMALL>(p, dtype);
+    return (int)hipGetLastError();
+}
+
+// The decode MLP's gate_up GEMV with SiLU * up in its epilogue: w [2I, K] (gate rows, then up rows), h [M, I] =
+// silu(g) * u as silu_mul_quant forms it before quantizing (g, u rounded as w8a8_gemv writes them), so that
+// per_token_quant(h) equals silu_mul_quant(w8a8_gemv output) bit for bit.  Taken where the VALU GEMV takes M and K
+// (M <= 5; K <= 17408 at one row, 8192 at two or three, 5120 at four or five): 1 = cannot implement otherwise.
+// No counterpart in the reference (whose MLP runs the GEMV and silu_quant.cu:71 as two launches).
+extern "C" int w8a8_gemv_silu(const void* a, const void* w, const void* sa, const void* sw, const void* bias, void* h,
+                              int M, int I, int K, int sa_rows, int sw_rows, int dtype, void* stream) {
+    if (I < 1 || M > 16 || check_common(a, w, M, 2 * I, K, dtype) != 0 || !h) return -1;
+    const Args p{(const int8_t*)a, (const int8_t*)w, (const float*)sa, (const float*)sw, (const uint16_t*)bias, h, M,
+                 I, K, sa_rows, sw_rows, (hipStream_t)stream};
+    if (!dot4_ok(p)) return 1;
+    if (dtype == DT_F16) launch_dot4_silu<f16>(p);
+    else launch_dot4_silu<bf16>(p);
     return (int)hipGetLastError();
 }
 

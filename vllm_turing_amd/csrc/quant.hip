@@ -102,18 +102,7 @@ __global__ void __launch_bounds__(256) per_token_quant_any_kernel(const uint16_t
     for (int k = threadIdx.x; k < K; k += blockDim.x) q[row * (long)K + k] = (int8_t)q8(to_float(T{xr[k]}) * inv);
 }
 
-// ---- SiLU(gate) * up + per-token quant -------------------------------------------------------------------------------
-__device__ __forceinline__ float silu_f(float f) {
-    const float e = expf(-f);                               // HIP's float32 exp (within 2 float32 ulps here)
-    const float d = 1.0f + e;
-    return f / d;                                           // IEEE division
-}
-
-template <typename T>
-__device__ __forceinline__ uint16_t silu_mul(float g, float u) {
-    const uint16_t sh = from_float<T>(silu_f(g));
-    return from_float<T>(to_float(T{sh}) * u);            // exact float product of two 16-bit values, one rounding
-}
+// ---- SiLU(gate) * up + per-token quant (silu_f, silu_mul: common.h) -------------------------------------------------
 
 template <typename T, int VPT>
 __global__ void __launch_bounds__(1024) silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,

@@ -8,7 +8,7 @@ and not part of this path.
 """
 import torch
 
-from . import _lib
+from . import _lib, w8a8
 from .normquant import rms_norm_dynamic_per_token_quant
 from .quantfuse import per_token_quant
 from .w8a8 import cutlass_scaled_mm
@@ -48,10 +48,67 @@ def silu_mul_quant(gate_up: torch.Tensor):
     return q, sc
 
 
+_flib.define("gemv_silu_(Tensor(a!) h, Tensor a, Tensor w, Tensor a_scales, Tensor w_scales) -> ()")
+
+
+def _gemv_silu_hip(h, a, w, a_scales, w_scales):
+    M, K = a.shape
+    if M == 0:
+        return
+    rc = _lib.lib().w8a8_gemv_silu(a.data_ptr(), w.data_ptr(), a_scales.data_ptr(), w_scales.data_ptr(), None,
+                                   h.data_ptr(), M, w.shape[0] // 2, K, int(a_scales.numel() > 1),
+                                   int(w_scales.numel() > 1), _lib.dtype_code(h.dtype), _lib.stream_handle(a.device))
+    if rc != 0:
+        raise RuntimeError(f"w8a8_gemv_silu failed: {rc}")
+
+
+torch.library.impl(_flib, "gemv_silu_", "CUDA")(_gemv_silu_hip)
+
+
+@torch.library.register_fake("vllm_turing_amd::gemv_silu_")
+def _gemv_silu_fake(h, a, w, a_scales, w_scales):
+    return None
+
+
+GEMV_SILU_MAX_M = 5
+
+
+def gemv_silu_ok(x_q, x_s, w_gate_up, sw_gate_up):
+    """Whether w8a8_gemv_silu takes the gate_up projection: the reference would run it on w8a8_gemv (M <= the GEMV
+    bound), the VALU GEMV takes M and K (M <= 5; K <= 17408 at one row, 8192 at two or three, 5120 above), and the
+    layouts are the GEMV's (int8 [M, K] and [2I, K] contiguous, float32 scales of M or 1 and 2I or 1)."""
+    M, K = x_q.shape
+    kmax = 17408 if M == 1 else 8192 if M <= 3 else 5120
+    N2 = w_gate_up.shape[0]
+    return (1 <= M <= min(GEMV_SILU_MAX_M, w8a8.MAX_M) and K % 16 == 0 and K <= kmax and N2 % 2 == 0
+            and x_q.dtype == torch.int8 and x_q.is_contiguous() and w_gate_up.dtype == torch.int8
+            and w_gate_up.is_contiguous() and w_gate_up.shape[1] == K
+            and x_q.data_ptr() % 16 == 0 and w_gate_up.data_ptr() % 16 == 0
+            and x_s.dtype == torch.float32 and x_s.is_contiguous() and x_s.numel() in (1, M)
+            and sw_gate_up.dtype == torch.float32 and sw_gate_up.is_contiguous() and sw_gate_up.numel() in (1, N2))
+
+
+def gemv_silu(x_q, x_s, w_gate_up, sw_gate_up, out_dtype):
+    """The decode MLP's first half in one launch: int8 x_q [M, K] times the gate_up weight [2I, K] with the GEMV's
+    small-M epilogue, then SiLU(gate) * up rounded as silu_mul_quant rounds it before quantizing -> [M, I] in
+    out_dtype.  per_token_quant of the result equals silu_mul_quant of the GEMV's output bit for bit."""
+    h = torch.empty((x_q.shape[0], w_gate_up.shape[0] // 2), dtype=out_dtype, device=x_q.device)
+    torch.ops.vllm_turing_amd.gemv_silu_(h, x_q, w_gate_up, x_s, sw_gate_up)
+    return h
+
+
 def mlp_quantized(x_q, x_s, w_gate_up, sw_gate_up, w_down, sw_down, out_dtype):
     """The quantized MLP of vllm_turing/tailoverlap.py:146-151 from an int8 input:
     gate_up = W8A8(x_q, w_gate_up) -> (a_q, a_s) = silu_mul_quant(gate_up) -> W8A8(a_q, w_down).
-    w_* are int8 [N, K] row-major weights, sw_* float32 [N, 1] scales."""
+    w_* are int8 [N, K] row-major weights, sw_* float32 [N, 1] scales.  At decode row counts the same chain runs as
+    two launches with the same bits: gemv_silu (SiLU * up in the gate_up GEMV's epilogue), then gemv_quant (the
+    down GEMV quantizing its input itself)."""
+    if gemv_silu_ok(x_q, x_s, w_gate_up, sw_gate_up):
+        h = gemv_silu(x_q, x_s, w_gate_up, sw_gate_up, out_dtype)
+        if w8a8.gemv_quant_ok(h, w_down, sw_down, None):
+            return w8a8.gemv_quant(h, w_down, sw_down)
+        a_q, a_s = per_token_quant(h)
+        return cutlass_scaled_mm(a_q, w_down.t(), a_s, sw_down, out_dtype)
     gate_up = cutlass_scaled_mm(x_q, w_gate_up.t(), x_s, sw_gate_up, out_dtype)
     a_q, a_s = silu_mul_quant(gate_up)
     return cutlass_scaled_mm(a_q, w_down.t(), a_s, sw_down, out_dtype)
