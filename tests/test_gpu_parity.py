@@ -822,6 +822,37 @@ def test_split_shared_workspace_and_graph(L):
     assert int(ws[:4096].count_nonzero()) == 0
 
 
+def test_workspace_cache(L):
+    """The package's K-split workspaces: one per stream, zeroed, at most WS_STREAMS kept, and the one a captured graph
+    uses kept whatever other streams come after."""
+    say("workspace cache")
+    from vllm_turing_amd import w8a8
+    dev = torch.device(DEV, torch.cuda.current_device())
+    w8a8._WS.clear()
+    w8a8._WS_IN_GRAPHS.clear()
+    shape = (512, 12288, 5120)
+    graph_stream = torch.cuda.Stream()
+    with torch.cuda.stream(graph_stream):
+        ws0 = w8a8.workspace(*shape, dev)               # allocated before the capture
+    y = torch.zeros(16, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=graph_stream):
+        assert w8a8.workspace(*shape, dev) is ws0
+        y.add_(1)
+    key = (dev.index, graph_stream.cuda_stream)
+    assert key in w8a8._WS_IN_GRAPHS
+    got, streams = [], [torch.cuda.Stream() for _ in range(w8a8.WS_STREAMS + 3)]   # kept: distinct handles
+    for s in streams:
+        with torch.cuda.stream(s):
+            got.append(w8a8.workspace(*shape, dev))
+    assert len(w8a8._WS) == w8a8.WS_STREAMS + 1 and w8a8._WS[key] is ws0
+    assert all(int(t[:4096].count_nonzero()) == 0 for t in got)
+    assert w8a8.workspace(4096, 12288, 5120, dev) is None   # three whole rounds: no split, no workspace
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.ones(16, device=DEV))
+
+
 GEMV_QUANT_CASES = [
     # M, N, K, dtype, ldx extra, bias, zero row
     (1, 5120, 6144, torch.bfloat16, 0, False, False),     # out_proj / o_proj at M = 1

@@ -19,6 +19,7 @@ The predicates gemv_ok / mma_ok / big_ok keep the reference's layout requirement
 Operands that fail them are made conforming (contiguous copies, zero padding of K to a multiple of 16) for the
 general kernel.  Every path runs a HIP kernel; there is no torch fallback.
 """
+import collections
 import os
 
 import torch
@@ -91,25 +92,35 @@ def mma(out, a, b, sa, sb, bias):
                           _lib.stream_handle(a.device)), "w8a8_mma launch")
 
 
-_WS = {}
+_WS = collections.OrderedDict()
+_WS_IN_GRAPHS = set()          # workspaces a captured graph uses: kept for the life of the process
+WS_STREAMS = 8                 # workspaces kept besides those (the most recently used streams)
 
 
 def workspace(M, N, K, device):
     """The K-split workspace w8a8_scaled_mm_ws takes for M x N x K on `device`'s current stream (one per device and
     stream, zeroed once, sized for the largest split plan), or None: when the shape does not split, or when the stream
-    has none yet and is capturing a graph (a zero fill recorded there would run only at replay)."""
+    has none yet and is capturing a graph (a zero fill recorded there would run only at replay).  Besides those a graph
+    has captured, at most WS_STREAMS are kept; dropping one is safe, as torch's allocator hands its memory only to
+    later allocations on the same stream, which run behind the work already queued there."""
     need = lib().w8a8_scaled_mm_ws_size(M, N, K)
     if need <= 0:
         return None
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
     ws = _WS.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
     if ws is None or ws.numel() < need:
-        if torch.cuda.is_current_stream_capturing():
+        if capturing:
             return None
         cus = torch.cuda.get_device_properties(device).multi_processor_count
         ws = torch.zeros(max(need, 4096 + cus * 262144), dtype=torch.uint8, device=device)
         _WS[key] = ws
+    if capturing:
+        _WS_IN_GRAPHS.add(key)
+    _WS.move_to_end(key)
+    for k in [k for k in _WS if k not in _WS_IN_GRAPHS][:-WS_STREAMS]:
+        del _WS[k]
     return ws
 
 
