@@ -193,3 +193,63 @@ def test_stack_pass_m4(L):
     torch.cuda.empty_cache()
     assert torch.equal(r_gpu, rc), f"residual stream: {int((r_gpu != rc).sum())} of {rc.numel()} differ"
     assert torch.equal(h_gpu, hc), f"hidden state: {int((h_gpu != hc).sum())} of {hc.numel()} differ"
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the reference's own test grids (tests/test_w8a8.py:11-12,30 and tests/test_w8a8_big.py:14-15,34), every output
+# against the oracle instead of vLLM's CUTLASS op
+# ---------------------------------------------------------------------------------------------------------------------
+def int_mm(a, w):
+    """Exact int32 a [M, K] x w [N, K]^T on the CPU (torch._int_mm, rows padded to 32 for its small-M limit)."""
+    M = a.shape[0]
+    if M >= 32:
+        return torch._int_mm(a, w.t().contiguous())
+    ap = torch.zeros(32, a.shape[1], dtype=torch.int8)
+    ap[:M] = a
+    return torch._int_mm(ap, w.t().contiguous())[:M]
+
+
+SMALL_M_SHAPES = [(8192, 5120), (5120, 3072), (7168, 5120), (17408, 5120), (5120, 8704)]   # TP2 (o_proj = out_proj)
+
+
+@pytest.mark.parametrize("N,K", SMALL_M_SHAPES)
+def test_reference_small_m_grid(L, N, K):
+    """tests/test_w8a8.py's grid: M in {1, 3, 4, 5, 6, 8, 10, 14, 16} at the TP2 shapes, a and W uniform in [-128,
+    128), sa = rand * 1e-2, sb = rand * 1e-3, fp16 out through the dispatch (the GEMV / MMA small-M chain)."""
+    from vllm_turing_amd import cutlass_scaled_mm
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    sb = torch.rand(N, 1, generator=g) * 1e-3
+    wd, sbd = w.to(DEV), sb.to(DEV)
+    for M in (1, 3, 4, 5, 6, 8, 10, 14, 16):
+        say(f"reference small-M grid N={N} K={K} M={M}")
+        a = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+        sa = torch.rand(M, 1, generator=g) * 1e-2
+        out = cutlass_scaled_mm(a.to(DEV), wd.t(), sa.to(DEV), sbd, torch.float16)
+        ref = oracle.epilogue(int_mm(a, w).numpy(), sa.numpy(), sb.numpy(), None, oracle.FP16, oracle.ORDER_SMALL_M)
+        assert np.array_equal(bits(out), ref), f"M={M}: {ndiff(bits(out), ref)} of {ref.size} differ"
+
+
+BIG_SHAPES = [(8704, 5120), (5120, 8704), (8192, 5120), (5120, 3072), (3584, 5120)]   # TP2 (o_proj = out_proj)
+
+
+@pytest.mark.parametrize("M", [1680, 4096, 6720])
+def test_reference_big_grid(L, M):
+    """tests/test_w8a8_big.py's grid: M in {1680, 4096, 6720} at its TP2 shapes, fp16 and bf16 out, through the
+    dispatch's large-M path (w8a8_big's kernels with the K-split workspace); every output bit for bit."""
+    from vllm_turing_amd import cutlass_scaled_mm
+    g = torch.Generator().manual_seed(M)
+    a = torch.randint(-128, 128, (M, 8704), dtype=torch.int8, generator=g)
+    sa = torch.rand(M, 1, generator=g) * 1e-2
+    ad, sad = a.to(DEV), sa.to(DEV)
+    for i, (N, K) in enumerate(BIG_SHAPES):
+        dt = torch.float16 if i % 2 == 0 else torch.bfloat16
+        say(f"reference big grid M={M} N={N} K={K} {dt}")
+        w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+        sb = torch.rand(N, 1, generator=g) * 1e-3
+        ak = ad[:, :K].contiguous()
+        out = cutlass_scaled_mm(ak, w.to(DEV).t(), sad, sb.to(DEV), dt)
+        acc = int_mm(a[:, :K].contiguous(), w)
+        ref = oracle.epilogue(acc.numpy(), sa.numpy(), sb.numpy(), None,
+                              oracle.FP16 if dt == torch.float16 else oracle.BF16, oracle.ORDER_LARGE_M)
+        assert np.array_equal(bits(out), ref), f"N={N} K={K}: {ndiff(bits(out), ref)} of {ref.size} differ"
