@@ -244,7 +244,7 @@ def workspace(torch, dev):
 
 def scaled_mm_ws(L, st, a_q, w, a_s, sw, bias, out, M, N, K, dtype_code):
     """The large-M W8A8 GEMM as the package runs it: w8a8_scaled_mm_ws with the workspace (the whole rounds of super
-    tiles, then the last partial round split over K)."""
+    tiles, then the last partial round split over K; 64-row tiles split over K where they fit two per CU)."""
     ws = _WS[0]
     return L.w8a8_scaled_mm_ws(a_q.data_ptr(), w.data_ptr(), a_s.data_ptr(), sw.data_ptr(),
                                None if bias is None else bias.data_ptr(), out.data_ptr(), M, N, K, 1, 1, dtype_code,
@@ -478,13 +478,15 @@ def bench_headline(torch, L, st, dev, args):
 
     # the other decode batch sizes of the same projection (M = 2, 4, 8), same weights and method
     decode_m = {}
+    workspace(torch, dev)
     for Md in (2, 4, 8, 16, 32, 64):
         cd = workloads.decode(Md)
         xq_d, xs_d = per_token_quant(cd["x"].to(dev))
         out_d = torch.empty(Md, N, dtype=torch.float16, device=dev)
 
         def gemv_d(i, Md=Md, xq_d=xq_d, xs_d=xs_d, out_d=out_d):
-            # the entry the reference's dispatch takes at this M (w8a8.py:108-117): GEMV, mid-band MMA, big GEMM
+            # the entry the reference's dispatch takes at this M (w8a8.py:108-117): GEMV, mid-band MMA, and above
+            # w8a8_big's kernels through the workspace entry, as the package's layers call them
             if Md <= 12:
                 rc = L.w8a8_gemv(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(), None,
                                  out_d.data_ptr(), Md, N, K, 1, 1, 0, st())
@@ -492,8 +494,7 @@ def bench_headline(torch, L, st, dev, args):
                 rc = L.w8a8_mma(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(), None,
                                 out_d.data_ptr(), Md, N, K, 1, 1, 0, st())
             else:
-                rc = L.w8a8_big(xq_d.data_ptr(), ws[i % copies].data_ptr(), xs_d.data_ptr(), sw.data_ptr(),
-                                out_d.data_ptr(), Md, N, K, 0, st())
+                rc = scaled_mm_ws(L, st, xq_d, ws[i % copies], xs_d, sw, None, out_d, Md, N, K, 0)
             if rc != 0:
                 raise RuntimeError(f"decode M={Md}: {rc}")
 
@@ -665,7 +666,8 @@ def bench_headline(torch, L, st, dev, args):
         "cpu_baseline": cpu,
         "gemv_read_ceiling": read_ceiling,
         "decode_other_m": {"workload": f"decode W8A8 K={K} N={N}, fp16 out, same rotated weights, the entry the reference "
-                                       f"dispatches at each M (w8a8_gemv <= 12, w8a8_mma <= 32, w8a8_big above)",
+                                       f"dispatches at each M (w8a8_gemv <= 12, w8a8_mma <= 32, above w8a8_big's "
+                                       f"kernels through the workspace entry, split over K where the plan splits)",
                            **decode_m},
         "gemm": {"workload": f"prefill W8A8 GEMM M={Mg} K={Kg} N={Ng}, bias, bf16 out, {gcopies} rotated weight copies "
                              f"({gcopies * Ng * Kg / 1e6:.0f} MB > 256 MB MALL)", "ms": round(ms_gemm, 4),

@@ -69,6 +69,13 @@ def test_argument_validation_codes(L):
     assert L.w8a8_scaled_mm_ws_size(200, 1024, 5120) == 0       # a mid-M shape: no split
     assert L.w8a8_scaled_mm_ws_size(4096, 12288, 5120) == 0     # 768 super tiles: whole rounds on 256 CUs
     assert L.w8a8_scaled_mm_ws_size(512, 12288, 512) == 0       # 4 K stages: pieces would be under 4 stages
+    # 64-row tiles over more than 12288 weight rows: two K pieces where they fit two per CU (256 CUs), 16 KB each
+    assert L.w8a8_scaled_mm_ws_size(64, 16384, 5120) == 4096 + 256 * 2 * 16384
+    assert L.w8a8_scaled_mm_ws_size(33, 17408, 5120) == 4096 + 272 * 2 * 16384
+    assert L.w8a8_scaled_mm_ws_size(64, 24576, 5120) == 0       # 384 tiles: more than two per CU already
+    assert L.w8a8_scaled_mm_ws_size(96, 13312, 5120) == 0       # two tile rows: 416 tiles
+    assert L.w8a8_scaled_mm_ws_size(64, 16384, 2048) == 0       # 16 stages: pieces of 8
+    assert L.w8a8_scaled_mm_ws_size(32, 16384, 5120) == 0       # 32 rows run on the streaming kernel
     # w8a8_gemv_silu: -1 on bad arguments, 1 where the VALU GEMV does not take M or K
     assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 0, 5120, 1, 1, 0, None) == -1      # I < 1
     assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 64, 40, 1, 1, 0, None) == -1      # K % 16

@@ -1,6 +1,6 @@
 """The allocation-free entry point w8a8_scaled_mm_noalloc (the library's per-GPU scratch in place of a workspace)
 against w8a8_scaled_mm_ws with a workspace of its own: the same 16-bit outputs and int32 accumulators bit for bit, on
-two calls in a row, the second smaller, and the tile counters of the workspace left at zero by both."""
+three calls in a row, each smaller than the one before, and the tile counters of the workspace left at zero by all."""
 import numpy as np
 import pytest
 import torch
@@ -25,9 +25,9 @@ def bits(t):
 def test_noalloc_matches_workspace_entry(L):
     st = torch.cuda.current_stream().cuda_stream
     g = torch.Generator().manual_seed(11)
-    # two calls in a row, the second with a smaller input; both split over K (M=4096, N=5120, K=17408: 256 whole tiles
-    # + 64 x 4 pieces, every slot of the scratch; M=512: 96 x 2 pieces)
-    for M, N, K in ((4096, 5120, 17408), (512, 12288, 5120)):
+    # three calls in a row, each with a smaller input; all split over K (M=4096, N=5120, K=17408: 256 whole tiles
+    # + 64 x 4 pieces, every slot of the scratch; M=512: 96 x 2 pieces; M=64: 256 64 x 64 tiles x 2 pieces)
+    for M, N, K in ((4096, 5120, 17408), (512, 12288, 5120), (64, 16384, 5120)):
         print(f"noalloc M={M} N={N} K={K}", flush=True)
         need = L.w8a8_scaled_mm_ws_size(M, N, K)
         assert need > 4096

@@ -481,14 +481,76 @@ __device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rs, uint8_t* ds
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, voff, k0, 0, 0);
 }
 
+// K-split workspace: SPLIT_HEAD_INTS tile counters (zero between calls), then for split tile rt its `splits` slots of
+// int32 accumulators, one per K piece, at rt * splits * (slot ints) past the counters.
+constexpr int SPLIT_HEAD_INTS = 1024;
+constexpr int SPLIT_SLOT_INTS = SUPER * SUPER;           // one super tile of int32 accumulators (256 KB)
+
+// The partial exchange of a K-split tile.  Piece `piece` of tile rt stores this workgroup's int32 accumulators to its
+// slot and arrives at the tile's counter; the last to arrive adds the other pieces' slots to its own accumulators
+// (integer sums: the result is the same in any order) and sets the counter back to zero.  Returns whether this
+// workgroup arrived last, i.e. holds the tile's whole sum and runs the epilogue.  No workgroup waits for another.
+// The slots are written and read with agent-coherent accesses (the sc1 form the compiler gives relaxed agent-scope
+// atomic stores and loads), so a piece's slot is visible on every XCD once its stores complete, without an L2
+// write-back or invalidation (the compiler's agent-scope fences do both, for the whole L2, and made the K split slower
+// than no split).  Each wavefront waits for its own stores; the barrier then orders them before the tile's arrival, and
+// the last piece's reads after it.  Slot layout: WAVES blocks of FM FN 4 KB, one per wavefront in its fragment order,
+// 1 KB per store instruction (lane l at 16 l).
+template <int FM, int FN, int WAVES>
+__device__ __forceinline__ bool split_exchange(v16i (&acc)[FM][FN], int* ws, int rt, int piece, int splits, int wave,
+                                               int lane, int tid) {
+    constexpr int WAVE_V4 = FM * FN * 4 * 64;            // 16-byte vectors per wavefront
+    constexpr long SLOT_INTS = (long)WAVES * WAVE_V4 * 4;
+    constexpr int CPOL_SC1 = 16;
+    const __amdgpu_buffer_rsrc_t rsp =
+        make_rsrc(ws + SPLIT_HEAD_INTS + (long)rt * splits * SLOT_INTS, (long)splits * SLOT_INTS * 4);
+    auto voff = [&](int q, int f, int c) { return ((q * WAVES + wave) * WAVE_V4 + (f * 4 + c) * 64 + lane) * 16; };
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v4i{acc[i][j][4 * c], acc[i][j][4 * c + 1], acc[i][j][4 * c + 2], acc[i][j][4 * c + 3]}, rsp,
+                    voff(piece, i * FN + j, c), 0, CPOL_SC1);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __shared__ int last;
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(ws + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    __syncthreads();
+    if (!last) return false;
+    for (int q = 0; q < splits; ++q) {
+        if (q == piece) continue;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsp, voff(q, i * FN + j, c), 0, CPOL_SC1);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * c + e] += v[e];
+                }
+    }
+    if (tid == 0) __hip_atomic_store(ws + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // WM x WN wavefronts (main configuration 2 x 4: two per SIMD, so one wavefront's LDS and barrier waits are covered by
 // the other's MFMAs).  Workgroup u of the grid computes quarter (or whole) tile u % SUB of super tile t_base + u / SUB.
+// KSPLIT (the mid configurations, `splits` K pieces): the grid is every BM x BN tile of the output times `splits`;
+// workgroup u (after the XCD remap) runs piece u / T of tile u % T (T tiles, column-major over the BM-row tile rows, so
+// that the tile rows of one weight column and the workgroups of one K range sit on one XCD) and meets the other pieces
+// in the workspace `ws` (split_exchange).
 template <typename T, int EPI, int WM, int WN, int FM, int FN, int KB, int NS, int SPLIT = 0, bool LEAD = false,
-          int GM = GROUP_M, bool PRIO = false>
+          int GM = GROUP_M, bool PRIO = false, bool KSPLIT = false>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                             const float* __restrict__ sa, const float* __restrict__ sw,
                                                             const uint16_t* __restrict__ bias, void* __restrict__ out,
-                                                            int M, int N, int K, int sa_rows, int sw_rows, int t_base) {
+                                                            int M, int N, int K, int sa_rows, int sw_rows, int t_base,
+                                                            int splits, int* __restrict__ ws) {
     extern __shared__ v4i ldsx[];
     // the wavefront index in a scalar register, so that what derives from it (the LDS block addresses of the
     // direct-to-LDS loads, the wavefront tile origins) is scalar too (M 4096 x N 12288 x K 5120: 228 -> 224 us;
@@ -500,16 +562,28 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 
     // XCD-aware remap: hardware places workgroup b on XCD b % 8; give each XCD a contiguous run of tiles (and the
     // SUB quarters of one super tile to the same XCD)
-    const int TM = (M + SUPER - 1) / SUPER, TN = (N + SUPER - 1) / SUPER;
     const int nb = gridDim.x, per = nb >> 3;
     int u = blockIdx.x;
     if (u < per * 8) u = (u & 7) * per + (u >> 3);
-    const int t = t_base + u / SUB, q = u % SUB;
-    const int gsz = GM * TN, grp = t / gsz, first_m = grp * GM;
-    const int gm = min(TM - first_m, GM);
-    const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
-    const int m0 = tm * SUPER + (q / (SUPER / BN)) * BM, n0 = tn * SUPER + (q % (SUPER / BN)) * BN;
-    if (m0 >= M || n0 >= N) return;                      // a quarter past the edge of the last super tile (uniform)
+    int m0, n0, kst0 = 0, nk = (K + KB - 1) / KB, piece = 0, rt = 0;   // tile origin, first stage and stage count
+    if constexpr (KSPLIT) {
+        const int TMb = (M + BM - 1) / BM, Tb = TMb * ((N + BN - 1) / BN);
+        piece = u / Tb;
+        rt = u % Tb;
+        m0 = (rt % TMb) * BM;
+        n0 = (rt / TMb) * BN;
+        kst0 = piece * nk / splits;
+        nk = (piece + 1) * nk / splits - kst0;           // >= 1: the host takes splits <= the stage count
+    } else {
+        const int TM = (M + SUPER - 1) / SUPER, TN = (N + SUPER - 1) / SUPER;
+        const int t = t_base + u / SUB, q = u % SUB;
+        const int gsz = GM * TN, grp = t / gsz, first_m = grp * GM;
+        const int gm = min(TM - first_m, GM);
+        const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
+        m0 = tm * SUPER + (q / (SUPER / BN)) * BM;
+        n0 = tn * SUPER + (q % (SUPER / BN)) * BN;
+        if (m0 >= M || n0 >= N) return;                  // a quarter past the edge of the last super tile (uniform)
+    }
 
     // global -> LDS directly (buffer_load_dwordx4 ... lds): one wavefront instruction fills 1 KB of LDS, i.e.
     // 1024 / KB rows of one stage; lane l lands at byte 16 l of it, so it fetches the logical chunk that the swizzle
@@ -599,10 +673,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
     constexpr int WAIT4 = waitcnt_vm(4 * Cfg::LPW), WAIT3 = waitcnt_vm(3 * Cfg::LPW);
     constexpr int WAIT2 = waitcnt_vm(2 * Cfg::LPW), WAIT1 = waitcnt_vm(Cfg::LPW), WAIT0 = waitcnt_vm(0);
     static_assert(4 * Cfg::LPW <= 63, "vmcnt range");
-    const int nk = (K + KB - 1) / KB;
+    const int kb0 = kst0 * KB;                           // this workgroup's first K byte
 #pragma unroll
     for (int s0 = 0; s0 < NS - 1; ++s0)
-        if (s0 < nk) issue(s0, s0 * KB);
+        if (s0 < nk) issue(s0, kb0 + s0 * KB);
     for (int kt = 0; kt < nk; ++kt) {
         // this wavefront's loads of stage kt are done once at most the later stages' loads (LPW each) remain
         const int ahead = min(nk - 1 - kt, NS - 2);
@@ -615,9 +689,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
         // __syncthreads() would also wait for the loads of the later stages still in flight.
         __builtin_amdgcn_s_barrier();
         const bool more = kt + NS - 1 < nk;
-        if (SPLIT == 0 && more) issue((kt + NS - 1) % NS, (kt + NS - 1) * KB);
-        if (SPLIT > 0 && LEAD && more) issue_slice((kt + NS - 1) % NS, (kt + NS - 1) * KB, 0);
-        compute(kt % NS, (kt + NS - 1) % NS, more ? (kt + NS - 1) * KB : -1);
+        if (SPLIT == 0 && more) issue((kt + NS - 1) % NS, kb0 + (kt + NS - 1) * KB);
+        if (SPLIT > 0 && LEAD && more) issue_slice((kt + NS - 1) % NS, kb0 + (kt + NS - 1) * KB, 0);
+        compute(kt % NS, (kt + NS - 1) % NS, more ? kb0 + (kt + NS - 1) * KB : -1);
+    }
+    if constexpr (KSPLIT) {
+        if (!split_exchange<FM, FN, WM * WN>(acc, ws, rt, piece, splits, wave, lane, tid)) return;
     }
 
     // D fragment of v_mfma_i32_32x32x32_i8 with the weights as the A operand: lane holds column lane % 32 of the
@@ -657,9 +734,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
 // t_base + full + u % rem, so that the workgroups of one XCD share K ranges).  Piece p runs stages
 // [p nk / splits, (p + 1) nk / splits), stores its int32 accumulators to its slot of the workspace and arrives at its
 // tile's counter; the last to arrive adds the other pieces' slots to its own accumulators (integer sums: the result is
-// the same in any order) and runs the epilogue, then sets the counter back to zero.  No workgroup waits for another.
-constexpr int SPLIT_HEAD_INTS = 1024;                    // workspace: tile counters, then the slots
-constexpr int SPLIT_SLOT_INTS = SUPER * SUPER;           // one super tile of int32 accumulators (256 KB)
+// the same in any order) and runs the epilogue, then sets the counter back to zero (split_exchange).  No workgroup waits
+// for another.
 template <typename T, int EPI, bool KFULL, bool SPLITK = false, int GM = GROUP_M, bool PRIO = true>
 __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                       const float* __restrict__ sa, const float* __restrict__ sw,
@@ -837,50 +913,8 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(const int8_t* __restrict__
     // reads of the stage buffers ended before the barrier closing slot 2 nk - 1, and each wavefront transposes through
     // its own LDS region, so no further barrier is needed (both groups passed 2 nk + 1).
 
-    if (split_role) {
-        // The slots are written and read with agent-coherent accesses (the sc1 form the compiler gives relaxed
-        // agent-scope atomic stores and loads), so a piece's slot is visible on every XCD once its stores complete,
-        // without an L2 write-back or invalidation (the compiler's agent-scope fences do both, for the whole L2, and
-        // made the K-split slower than no split).  Each wavefront waits for its own stores; the barrier then orders
-        // them before the tile's arrival, and the reads of the last piece after it.  Layout per piece: 32 KB per
-        // wavefront in its fragment order, 1 KB per store instruction (lane l at 16 l).
-        constexpr int WAVE_V4 = FM * FN * 4 * 64;
-        constexpr int CPOL_SC1 = 16;
-        const long tile_slot = (long)rt * splits;        // (slots and counters indexed from the first split tile)
-        const __amdgpu_buffer_rsrc_t rsp =
-            make_rsrc(ws + SPLIT_HEAD_INTS + tile_slot * SPLIT_SLOT_INTS, (long)splits * SPLIT_SLOT_INTS * 4);
-        auto voff = [&](int q, int f, int c) { return ((q * 8 + wave) * WAVE_V4 + (f * 4 + c) * 64 + lane) * 16; };
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        v4i{acc[i][j][4 * c], acc[i][j][4 * c + 1], acc[i][j][4 * c + 2], acc[i][j][4 * c + 3]}, rsp,
-                        voff(piece, i * FN + j, c), 0, CPOL_SC1);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-        __shared__ int last;
-        __syncthreads();
-        if (tid == 0)
-            last = __hip_atomic_fetch_add(ws + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
-        __syncthreads();
-        if (!last) return;
-        for (int q = 0; q < splits; ++q) {
-            if (q == piece) continue;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsp, voff(q, i * FN + j, c), 0, CPOL_SC1);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) acc[i][j][4 * c + e] += v[e];
-                    }
-        }
-        if (tid == 0) __hip_atomic_store(ws + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // (slots and counters indexed from the first split tile)
+    if (split_role && !split_exchange<FM, FN, WM * WN>(acc, ws, rt, piece, splits, wave, lane, tid)) return;
 
     const int mb = m0 + grp * WTM, nbw = n0 + gw * WTN;
     if constexpr (EPI == EPI_I32) {
@@ -1591,8 +1625,11 @@ struct MidCfg {
     static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 4, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
+#ifndef W8_MID64_NS
+#define W8_MID64_NS 4
+#endif
 struct Mid64Cfg {
-    static constexpr int WM = 2, WN = 2, FM = 1, FN = 1, KB = 128, NS = 4, SPLIT = 0;
+    static constexpr int WM = 2, WN = 2, FM = 1, FN = 1, KB = 128, NS = W8_MID64_NS, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
 constexpr int MID_GEMM_MAX_M = 128, MID_GEMM_WIDE_N = 12288;
@@ -1633,16 +1670,16 @@ static void launch_gemm_pp_split(const Args& p, int t_base, int full, int rem, i
     else launch_gemm_pp_k<T, EPI, false, true>(p, t_base, blocks, splits, full);
 }
 
-template <typename T, int EPI, typename C>
-static void launch_gemm_cfg(const Args& p, int t_base, int blocks) {
+template <typename T, int EPI, typename C, bool KS = false>
+static void launch_gemm_cfg(const Args& p, int t_base, int blocks, int splits = 1) {
     using G = GemmCfg<C::WM, C::WN, C::FM, C::FN, C::KB, C::NS>;
     const void* kern = reinterpret_cast<const void*>(
-        &gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD>);
+        &gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD, GROUP_M, false, KS>);
     static const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
     (void)attr;
-    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD>
+    gemm_kernel<T, EPI, C::WM, C::WN, C::FM, C::FN, C::KB, C::NS, C::SPLIT, C::LEAD, GROUP_M, false, KS>
         <<<blocks, G::THREADS, G::LDS_BYTES, p.st>>>(
-        p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base);
+        p.a, p.w, p.sa, p.sw, p.bias, p.out, p.M, p.N, p.K, p.sa_rows, p.sw_rows, t_base, splits, p.ws);
 }
 
 
@@ -1709,9 +1746,43 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
     return s;
 }
 
+// K split of the 64 x 64 mid tiles (33..64 rows against more than 12288 weight rows).  A workgroup of those tiles is
+// bound by its own stage loop rather than by HBM (at M = 64, K = 5120 the time grows ~20 us + bytes / 8.8 TB/s with
+// N), so two K pieces per tile halve each workgroup's loop where both pieces of every tile fit at two workgroups per
+// CU (64 KB of LDS each).  Same box, rotated weights, bf16 with bias, unsplit -> split: M 64 x N 16384 34.0 -> 25.2 us,
+// M 64 x N 12800 33.6 -> 23.8, M 48 x N 13312 30.8 -> 22.8, M 64 x N 13312 x K 17408 93.1 -> 59.8, M 64 x N 17408
+// (272 tiles) 35.1 -> 32.1, M 40 x N 17408 x K 17408 85.4 -> 76.0; three pieces tie with two at 272 tiles and lose up
+// to 17% below, four to eight lose more; more tiles than that lose (M 64 x N 24576 36.4 -> 41.0, M 128 x N 17408 42.3 -> 45.1), and 3 K stages (three
+// workgroups per CU) run the unsplit tiles 40% slower and the split ones no faster.
+#ifndef W8_MID_SPLIT
+#define W8_MID_SPLIT -1                                  // -1: mid_split_plan's choice; 0 or 1: none; s >= 2: s pieces
+#endif
+static bool mid64_path(int M, int N) { return M > 32 && M <= MID_GEMM_MAX_M && N > MID_GEMM_WIDE_N; }
+static int mid_split_plan(int M, int N, int K, int cus, long* bytes) {
+    *bytes = 0;
+    if (!mid64_path(M, N)) return 1;
+    const int tiles = ((M + 63) / 64) * ((N + 63) / 64), nk = (K + 127) / 128;
+    int s = W8_MID_SPLIT;
+    // two pieces where they fit two workgroups per CU in about one round (64 KB of LDS each) and stay >= 16 stages
+    if (s < 0) s = 16 * tiles <= 17 * cus && nk >= 32 ? 2 : 1;
+    // at most 4096 slots of 16 KB, so that any plan fits the allocation-free entry's scratch (64 MiB of slots)
+    s = min(min(s, nk), 4096 / tiles);
+    (void)cus;
+    if (s < 2 || tiles > SPLIT_HEAD_INTS) return 1;
+    *bytes = (long)SPLIT_HEAD_INTS * 4 + (long)tiles * s * 64 * 64 * 4;
+    return s;
+}
+
 template <typename T, int EPI>
 static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
-    if (policy == 1 && p.ws) {                           // the K-split remainder, when the caller gave a workspace
+    if (policy == 1 && p.ws) {                           // the K splits, when the caller gave a workspace
+        long mbytes;
+        const int ms = mid_split_plan(p.M, p.N, p.K, cu_count(), &mbytes);
+        if (ms >= 2 && mbytes <= p.ws_bytes) {
+            const int tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+            launch_gemm_cfg<T, EPI, Mid64Cfg, true>(p, 0, tiles * ms, ms);
+            return;
+        }
         int full, rem;
         long bytes;
         const int s = split_plan(p.M, p.N, p.K, cu_count(), &full, &rem, &bytes);
@@ -1891,13 +1962,15 @@ extern "C" int w8a8_scaled_mm(const void* a, const void* w, const void* sa, cons
 extern "C" long w8a8_scaled_mm_ws_size(int M, int N, int K) {
     if (M < 1 || N < 1 || K < 16) return -1;
     int full, rem;
-    long bytes;
+    long bytes, mbytes;
     split_plan(M, N, K, cu_count(), &full, &rem, &bytes);
-    return bytes;
+    mid_split_plan(M, N, K, cu_count(), &mbytes);
+    return max(bytes, mbytes);
 }
 
 // w8a8_scaled_mm with a workspace (16-byte aligned, ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K); its first 4 KB zero
-// before the first call, and every call leaves them zero) for the K-split remainder of the prefill GEMM; dtype 2
+// before the first call, and every call leaves them zero) for the prefill GEMM's K splits (split_plan for a last
+// partial round of super tiles, mid_split_plan for the 64 x 64 tiles of 33..64 rows); dtype 2
 // writes the raw int32 accumulators to out [M, N] instead (sa, sw, bias unused).  Calls that share a workspace must
 // not overlap.  Returns -1 on bad arguments (a workspace too small included), else the HIP error of the launches.
 extern "C" int w8a8_scaled_mm_ws(const void* a, const void* w, const void* sa, const void* sw, const void* bias,
