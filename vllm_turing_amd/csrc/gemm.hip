@@ -6,11 +6,13 @@
 // it, passed to cutlass_scaled_mm as its [K, N] stride-(1, K) view); sa: float32 [M] or [1]; sw: float32 [N] or [1];
 // bias: [N] of the output type or null; out: [M, N] fp16 or bf16.
 //
-// Five kernels:
+// Six kernels on the path (and two helpers: hbm_read_kernel, the M = 1 GEMV's weight stream without its math, the
+// read ceiling the benchmark reports; clear_ints_kernel, which zeroes the allocation-free entry's tile counters):
 //  * gemv_dot4_kernel, M = 1 and K <= 17408, M = 2, 3 and K <= 8192, M = 4, 5 and K <= 5120 (decode): weight-streaming
 //    through the VALU: each wavefront instruction reads 1 KB contiguous of one weight row, v_dot4_i32_i8 against
 //    activations held in registers, wavefront reduction with DPP / ds_swizzle.  Small-M epilogue chain
-//    (csrc/w8a8_gemv.cu:91).
+//    (csrc/w8a8_gemv.cu:91).  Two fused forms: QX quantizes 16-bit activations per token in each workgroup's LDS
+//    first (w8a8_gemv_quant), SILU pairs each gate row with its up row and writes silu(g) * u (w8a8_gemv_silu).
 //  * stream_lds_kernel, the rest of M <= 32 (decode, speculative verify), and passes of up to 64 rows for 33..128 rows
 //    against small N: weight-streaming and HBM-bound.  A workgroup owns one to three 16-row weight tiles; its 4 (or 2)
 //    wavefronts take interleaved 128-byte K steps, each through a private LDS ring filled by direct-to-LDS loads of
@@ -23,17 +25,20 @@
 //  * w8a16_kernel (the int8 LM head, the rest of M <= 32): the LDS-ring weight stream (two or three 16-row tiles per
 //    workgroup sharing each activation fragment) with each int8 fragment widened to fp16 / bf16 in registers for
 //    v_mfma_f32_16x16x32_{f16,bf16}; float32 sums.
-//  * gemm_kernel, M > 32 (prefill): MFMA-bound.  256 x 256 output tiles, 8 wavefronts (two per SIMD) of 128 x 64,
-//    each a 4 x 2 grid of v_mfma_i32_32x32x32_i8; 128-byte K stages loaded straight from HBM into LDS
-//    (buffer_load ... lds), double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128
-//    conflict-free, and the operand fragments of the next 32-byte sub-step read from LDS during the current one's
-//    MFMAs; workgroups remapped so the tiles resident on one XCD share A rows and W rows in that XCD's L2.  Where the
-//    tiles leave a last partial round over the CUs, that round runs as 128 x 128 quarter tiles (4 wavefronts of
-//    64 x 64: two workgroups per CU, or one with 4 K stages in flight where they fit in one round), so it spreads
-//    over the whole chip.  33..128 rows (and 129..256 against small N) run on 64 x 128 or 64 x 64 tiles with 4 K
-//    stages in flight.  The next stage's loads go out in slices between the MFMA blocks of the first
-//    sub-steps.  The epilogue goes through LDS so that every global store writes whole lines, non-temporally.
-//    Large-M epilogue (csrc/w8a8_big.cu:26-35).
+//  * gemm_pp_kernel, M > 32 (prefill), the main configuration: MFMA-bound.  256 x 256 output tiles, 8 wavefronts of
+//    128 x 64 (each a 4 x 2 grid of v_mfma_i32_32x32x32_i8) in two groups of four, one of each per SIMD, that
+//    alternate between a compute phase (the MFMAs of one K stage from registers) and a memory phase (all operand
+//    fragments of the next stage from LDS); 128-byte K stages loaded straight from HBM into LDS (buffer_load ... lds),
+//    double-buffered (128 KB), with an XOR swizzle of the 16-byte chunks that keeps ds_read_b128 conflict-free;
+//    workgroups remapped so the tiles resident on one XCD share A rows and W rows in that XCD's L2.  With a
+//    workspace, a last partial round of tiles runs as K pieces whose int32 partial sums meet in it (split_exchange).
+//    The epilogue goes through LDS so that every global store writes whole lines, non-temporally.  Large-M epilogue
+//    (csrc/w8a8_big.cu:26-35).
+//  * gemm_kernel, the other prefill configurations: where the 256 x 256 tiles leave a last partial round over the
+//    CUs and no K split is taken, that round runs as 128 x 128 quarter tiles (4 wavefronts of 64 x 64: two
+//    workgroups per CU, or one with 4 K stages in flight where they fit in one round), so it spreads over the whole
+//    chip; 33..128 rows (and 129..256 against small N) run on 64 x 128 or 64 x 64 tiles with 4 K stages in flight,
+//    the 64 x 64 tiles of 33..64 rows as two K pieces where those fit two workgroups per CU.
 //
 // The kernels use the freedom that an integer dot product does not depend on the order of k: each lane feeds the
 // MFMA the same permutation of k on its A and B operands (the dot4 kernel pairs weight and activation chunks the
