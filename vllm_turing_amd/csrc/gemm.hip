@@ -1630,11 +1630,8 @@ struct MidCfg {
     static constexpr int WM = 2, WN = 2, FM = 1, FN = 2, KB = 128, NS = 4, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
-#ifndef W8_MID64_NS
-#define W8_MID64_NS 4
-#endif
 struct Mid64Cfg {
-    static constexpr int WM = 2, WN = 2, FM = 1, FN = 1, KB = 128, NS = W8_MID64_NS, SPLIT = 0;
+    static constexpr int WM = 2, WN = 2, FM = 1, FN = 1, KB = 128, NS = 4, SPLIT = 0;
     static constexpr bool LEAD = false;
 };
 constexpr int MID_GEMM_MAX_M = 128, MID_GEMM_WIDE_N = 12288;
@@ -1757,8 +1754,9 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
 // CU (64 KB of LDS each).  Same box, rotated weights, bf16 with bias, unsplit -> split: M 64 x N 16384 34.0 -> 25.2 us,
 // M 64 x N 12800 33.6 -> 23.8, M 48 x N 13312 30.8 -> 22.8, M 64 x N 13312 x K 17408 93.1 -> 59.8, M 64 x N 17408
 // (272 tiles) 35.1 -> 32.1, M 40 x N 17408 x K 17408 85.4 -> 76.0; three pieces tie with two at 272 tiles and lose up
-// to 17% below, four to eight lose more; more tiles than that lose (M 64 x N 24576 36.4 -> 41.0, M 128 x N 17408 42.3 -> 45.1), and 3 K stages (three
-// workgroups per CU) run the unsplit tiles 40% slower and the split ones no faster.
+// to 17% below, four to eight lose more; more tiles than that lose (M 64 x N 24576 36.4 -> 41.0, M 128 x N 17408
+// 42.3 -> 45.1), and 3 K stages (three workgroups per CU) run the unsplit tiles 40% slower and the split ones no
+// faster.
 #ifndef W8_MID_SPLIT
 #define W8_MID_SPLIT -1                                  // -1: mid_split_plan's choice; 0 or 1: none; s >= 2: s pieces
 #endif
@@ -1772,7 +1770,6 @@ static int mid_split_plan(int M, int N, int K, int cus, long* bytes) {
     if (s < 0) s = 16 * tiles <= 17 * cus && nk >= 32 ? 2 : 1;
     // at most 4096 slots of 16 KB, so that any plan fits the allocation-free entry's scratch (64 MiB of slots)
     s = min(min(s, nk), 4096 / tiles);
-    (void)cus;
     if (s < 2 || tiles > SPLIT_HEAD_INTS) return 1;
     *bytes = (long)SPLIT_HEAD_INTS * 4 + (long)tiles * s * 64 * 64 * 4;
     return s;
