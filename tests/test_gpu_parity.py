@@ -867,6 +867,8 @@ GEMV_QUANT_CASES = [
     (1, 5120, 17408, torch.float16, 0, False, False),     # the longest K of the fused kernel at one row
     (5, 333, 5120, torch.float16, 0, True, True),
     (1, 96, 272, torch.bfloat16, 0, False, False),        # K not a multiple of the 1 KB row chunk
+    (1, 5120, 17408, torch.bfloat16, 64, True, True),     # the fused kernel: strided row, bias, an all-zero row
+    (1, 2000, 16400, torch.float16, 8, True, False),      # the fused kernel: K past every thread's full share
     (8, 4096, 5120, torch.bfloat16, 0, False, True),      # M = 8: fallback
     (12, 2048, 1024, torch.float16, 16, True, False),
 ]

@@ -115,6 +115,7 @@ __device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sa
 // pair (p, p + N) (R = 2); instead of the two outputs the kernel writes out[m, p] = silu(g) * u in 16 bits, with g and
 // u rounded as the GEMV writes them and the product as silu_mul_quant forms it before quantizing
 // (vllm_turing/csrc/silu_quant.cu:39), so the decode MLP needs no separate SiLU kernel.
+constexpr int QX_THREADS = 256;                          // threads of a workgroup of the fused-quant GEMV
 template <typename T, int M, int CH, int R, int EPI, bool NT = true, bool QX = false, bool SILU = false>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
@@ -205,17 +206,24 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
         // absmax over the row (wavefront max, then across the wavefronts), then the int8 values from a second read
         // of the same (now cached) row; the wavefronts then take their chunks from LDS.  Workgroup 0 also writes
         // the int8 rows and scales out.
+        // Each thread loads its whole share of the row (at most XV vectors of 8 values; chunks past the row re-read
+        // its last vector, which leaves the maximum unchanged and is not stored) before using any of it, so the
+        // prologue waits for one round of loads instead of one per vector and reads the row once.
         extern __shared__ v4i xq_lds[];
         int8_t* xl = reinterpret_cast<int8_t*>(xq_lds);
         float* red = reinterpret_cast<float*>(xl + M * K);   // one float per wavefront
-        const int nthr = blockDim.x, tid = threadIdx.x, nvec = K >> 3;
+        constexpr int nthr = QX_THREADS, XV = (CH * 128 + QX_THREADS - 1) / QX_THREADS;   // K <= CH * 1024
+        const int tid = threadIdx.x, nvec = K >> 3;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const uint4* xr = reinterpret_cast<const uint4*>(x + m * ldx);
+            uint4 xv[XV];
+#pragma unroll
+            for (int i = 0; i < XV; ++i) xv[i] = xr[min(tid + i * nthr, nvec - 1)];
             float amax = 0.0f;
-            for (int v = tid; v < nvec; v += nthr) {
-                const uint4 u = xr[v];
-                const uint32_t e4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < XV; ++i) {
+                const uint32_t e4[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     amax = __builtin_fmaxf(amax, __builtin_fabsf(lo_half(e4[e], T{})));
@@ -223,17 +231,18 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
                 }
             }
             amax = wave_max(amax);
-            if (nthr > 64) {
-                if (lane == 0) red[threadIdx.x >> 6] = amax;
-                __syncthreads();
-                for (int i = 0; i < (nthr >> 6); ++i) amax = __builtin_fmaxf(amax, red[i]);
-                __syncthreads();                         // red is reused by the next row
-            }
+            if (lane == 0) red[threadIdx.x >> 6] = amax;
+            __syncthreads();
+            for (int i = 0; i < (nthr >> 6); ++i) amax = __builtin_fmaxf(amax, red[i]);
+            __syncthreads();                             // red is reused by the next row
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
             sam[m] = amax / 127.0f;
             if (blockIdx.x == 0 && tid == 0) xs[m] = sam[m];
-            for (int v = tid; v < nvec; v += nthr) {
-                const uint4 u = xr[v];
+#pragma unroll
+            for (int i = 0; i < XV; ++i) {
+                const int v = tid + i * nthr;
+                if (v >= nvec) break;
+                const uint4 u = xv[i];
                 const uint32_t e4[4] = {u.x, u.y, u.z, u.w};
                 int b[8];
 #pragma unroll
@@ -1413,8 +1422,8 @@ static void launch_dot4_ch(const Args& p) {
             const int lds = M * CH * 1024 + 64;          // rows of up to CH * 1024 int8, then the reduction floats
             static const int per_cu = [&] {
                 int nb = 0;
-                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), 256, lds) !=
-                        hipSuccess || nb < 1)
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), QX_THREADS,
+                                                                 lds) != hipSuccess || nb < 1)
                     nb = 1;
                 return nb < DOT4_BLOCKS_PER_CU ? nb : DOT4_BLOCKS_PER_CU;
             }();
@@ -1422,9 +1431,8 @@ static void launch_dot4_ch(const Args& p) {
             // so fewer, fuller workgroups (one row per wavefront: K = 6144, N = 5120 9.07 -> 8.55 us; K = 17408
             // 18.83 -> 18.62 us; two rows per wavefront no better)
             const int need = (p.N + 11) / 12, grid = cu_count() * per_cu;
-            kern<<<need < grid ? need : grid, 256, p.M * p.K + 64, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N,
-                                                                          p.K, p.sa_rows, p.sw_rows, p.x, p.ldx,
-                                                                          p.xq, p.xs);
+            kern<<<need < grid ? need : grid, QX_THREADS, p.M * p.K + 64, p.st>>>(
+                p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows, p.x, p.ldx, p.xq, p.xs);
             return;
         }
         if constexpr (M <= 2) {
