@@ -317,12 +317,12 @@ __global__ void __launch_bounds__(1024) rms_norm_quant_kernel(const uint16_t* __
     uint4 xv[VPT], rv[VPT], wv[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int idx = threadIdx.x + j * blockDim.x;
-        xv[j] = idx < nvec ? xr[idx] : make_uint4(0, 0, 0, 0);
-        rv[j] = RES && idx < nvec ? rr[idx] : make_uint4(0, 0, 0, 0);
-        // the norm weights with the row (unconditional, an in-bounds vector past the row's end): loaded where they are
-        // used, under the idx < nvec branch, each load was waited for on its own
-        wv[j] = w4[min(idx, nvec - 1)];
+        // every load unconditional (an in-bounds vector past the row's end, masked where used): a conditional load
+        // made the compiler wait for the row and the residual before issuing the norm weights' load
+        const int idx = min((int)threadIdx.x + j * (int)blockDim.x, nvec - 1);
+        xv[j] = xr[idx];
+        rv[j] = RES ? rr[idx] : make_uint4(0, 0, 0, 0);
+        wv[j] = w4[idx];
     }
     auto sum_at = [&](int j, int e, bool hi) -> float {                  // s = float(x) + float(r), one rounding
         const uint32_t xw = e == 0 ? xv[j].x : e == 1 ? xv[j].y : e == 2 ? xv[j].z : xv[j].w;
