@@ -83,6 +83,13 @@ __device__ __forceinline__ v4i wload(const int8_t* p) {
 __device__ __align__(16) const uint16_t g_zero4[4] = {0, 0, 0, 0};
 // A 16-bit zero in device memory: the bias operand of a row without bias, so that the bias load is unconditional.
 __device__ const uint16_t g_zero16 = 0;
+// A value loaded through a global-address-space pointer: a load through a pointer the compiler cannot place (such as
+// a select between a kernel argument and g_zero16) becomes a FLAT load, which counts on two counters and completes
+// out of order, and then every wait for vector memory drains all loads in flight.
+template <typename V>
+__device__ __forceinline__ V gload(const void* p) {
+    return *(const __attribute__((address_space(1))) V*)p;
+}
 
 // Output write of one element as store_out, with the scales and bias already in registers.
 template <typename T, int EPI>
@@ -115,8 +122,12 @@ __device__ __forceinline__ void store_pre(void* out, long idx, int acc, float sa
 // pair (p, p + N) (R = 2); instead of the two outputs the kernel writes out[m, p] = silu(g) * u in 16 bits, with g and
 // u rounded as the GEMV writes them and the product as silu_mul_quant forms it before quantizing
 // (vllm_turing/csrc/silu_quant.cu:39), so the decode MLP needs no separate SiLU kernel.
+// DEF (the one-wavefront grid of M <= 2, whose launch gives every wavefront at most DEF = 3 row groups): the outputs
+// stay in registers and are stored after the last group.  An output store between two groups' loads keeps the
+// compiler from counting the loads still in flight (stores and loads complete out of order against each other), so
+// its wait before each group's math drained every load, and a wavefront had one group in flight instead of two.
 constexpr int QX_THREADS = 256;                          // threads of a workgroup of the fused-quant GEMV
-template <typename T, int M, int CH, int R, int EPI, bool NT = true, bool QX = false, bool SILU = false>
+template <typename T, int M, int CH, int R, int EPI, bool NT = true, bool QX = false, bool SILU = false, int DEF = 0>
 __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                                         const float* __restrict__ sa, const float* __restrict__ sw,
                                                         const uint16_t* __restrict__ bias, void* __restrict__ out,
@@ -151,7 +162,7 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
             // unconditional loads, converted only in finish: a conditional load or a conversion next to it would
             // make the compiler wait for the next row's weights as well
             swb[buf][r] = EPI == EPI_I32 ? 0.0f : sw[sw_rows ? n : 0];
-            bb[buf][r] = EPI == EPI_SMALL || EPI == EPI_LARGE_BIAS ? *(bias ? bias + n : &g_zero16) : 0;
+            bb[buf][r] = EPI == EPI_SMALL || EPI == EPI_LARGE_BIAS ? gload<uint16_t>(bias ? bias + n : &g_zero16) : 0;
         }
     };
     auto finish = [&](int buf, int n0) {
@@ -200,7 +211,9 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
         if (wid >= N) return;
     }
     const int cnt = wid < N ? (N - 1 - wid) / stride + 1 : 0;
-    load(0, wid);                                        // rows past N read row N - 1 (see load)
+    // rows past N read row N - 1 (see load).  With DEF the first group's loads follow the activations' (conditional)
+    // loads instead, so that the wait before its math can count the loads issued after it.
+    if constexpr (DEF == 0) load(0, wid);
     if constexpr (QX) {
         // The workgroup quantizes the rows once into LDS (xl: M rows of K int8), each thread 8 values per step:
         // absmax over the row (wavefront max, then across the wavefronts), then the int8 values from a second read
@@ -274,6 +287,63 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
             }
 #pragma unroll
         for (int m = 0; m < M; ++m) sam[m] = EPI == EPI_I32 ? 0.0f : sa[sa_rows ? m : 0];
+    }
+    if constexpr (DEF > 0) {
+        static_assert(DEF == 3 && !QX && !SILU, "deferred stores: the one-wavefront grid of M <= 2");
+        // the value lane r * M + m stores for output (m, n0 + r * nw) of the group in buffer buf
+        auto value = [&](int buf) {
+            int acc[R][M];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    int sum = 0;
+#pragma unroll
+                    for (int j = 0; j < CH; ++j) {
+                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].x, av[m][j].x, sum, false);
+                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].y, av[m][j].y, sum, false);
+                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].z, av[m][j].z, sum, false);
+                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].w, av[m][j].w, sum, false);
+                    }
+                    acc[r][m] = wave_sum(sum);
+                }
+            uint32_t v = 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    uint32_t x;
+                    if constexpr (EPI == EPI_I32) x = (uint32_t)acc[r][m];
+                    else if constexpr (EPI == EPI_SMALL)
+                        x = from_float<T>(epi_small(acc[r][m], sam[m], swb[buf][r], to_float(T{bb[buf][r]})));
+                    else if constexpr (EPI == EPI_LARGE) x = from_float<T>(epi_large(acc[r][m], sam[m], swb[buf][r]));
+                    else x = from_float<T>(epi_large_bias(acc[r][m], sam[m], swb[buf][r], to_float(T{bb[buf][r]})));
+                    v = lane == r * M + m ? x : v;
+                }
+            return v;
+        };
+        auto put = [&](uint32_t v, int n0) {
+            if (lane < R * M) {
+                const int r = lane / M, m = lane % M, n = n0 + r * nw;
+                if (n < N) {
+                    if constexpr (EPI == EPI_I32) static_cast<int*>(out)[(long)m * N + n] = (int)v;
+                    else static_cast<uint16_t*>(out)[(long)m * N + n] = (uint16_t)v;
+                }
+            }
+        };
+        // groups past cnt load row N - 1 (see load) and are not stored
+        load(0, wid);
+        load(1, wid + stride);
+        __builtin_amdgcn_sched_barrier(0);              // keep the loads ahead of the math
+        const uint32_t v0 = value(0);
+        load(0, wid + 2 * stride);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t v1 = value(1);
+        const uint32_t v2 = value(0);
+        put(v0, wid);
+        if (cnt > 1) put(v1, wid + stride);
+        if (cnt > 2) put(v2, wid + 2 * stride);
+        return;
     }
     int k = 0;
     for (; k + 2 < cnt; k += 2) {
@@ -388,7 +458,9 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[FM][FN], uint8_
             for (int q = 0; q < 4; ++q) {
                 const int n = min(nb + j * 32 + 8 * q + 4 * (lane >> 5), N - 4);
                 sw4[j][q] = *reinterpret_cast<const float4*>(sw + n);
-                b2[j][q] = *reinterpret_cast<const uint2*>(has_bias ? bias + n : g_zero4);
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));   // (a HIP uint2 loads as FLAT)
+                const u32x2 bv2 = gload<u32x2>(has_bias ? static_cast<const void*>(bias + n) : g_zero4);
+                b2[j][q] = make_uint2(bv2.x, bv2.y);
             }
     }
 #pragma unroll
@@ -1309,7 +1381,7 @@ __global__ void __launch_bounds__(256) w8a16_dot_kernel(const uint16_t* __restri
             wb[buf][j] = wload<true>(row + min(c, K16 - 1) * 16);   // unmasked (see gemv_dot4_kernel)
         }
         sb[buf] = s[sr];
-        bb[buf] = *(bias ? bias + sr : &g_zero16);       // unconditional (see gemv_dot4_kernel)
+        bb[buf] = gload<uint16_t>(bias ? bias + sr : &g_zero16);   // unconditional (see gemv_dot4_kernel)
     };
     auto finish = [&](int buf, int n) {
         float acc[M];
@@ -1435,10 +1507,11 @@ static void launch_dot4_ch(const Args& p) {
                 p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows, p.x, p.ldx, p.xq, p.xs);
             return;
         }
-        if constexpr (M <= 2) {
+        if constexpr (M <= 2) {                          // every wavefront DOT4_ROWS_PER_WAVE rows: stores deferred
+            static_assert(DOT4_ROWS_PER_WAVE == 3, "the deferred-store kernel takes three row groups");
             const int waves = (p.N + DOT4_ROWS_PER_WAVE - 1) / DOT4_ROWS_PER_WAVE;
-            kern<<<waves, 64, 0, p.st>>>(p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows, p.x,
-                                         p.ldx, p.xq, p.xs);
+            gemv_dot4_kernel<T, M, CH, 1, EPI, true, false, false, 3><<<waves, 64, 0, p.st>>>(
+                p.a, p.w, p.sa, p.sw, p.bias, p.out, p.N, p.K, p.sa_rows, p.sw_rows, p.x, p.ldx, p.xq, p.xs);
             return;
         }
         static const int per_cu = row_stream_per_cu(reinterpret_cast<const void*>(kern));
@@ -2119,14 +2192,17 @@ __global__ void __launch_bounds__(64) hbm_read_kernel(const int8_t* __restrict__
     const int cnt = (rows - 1 - wid) / nw + 1;
     load(0, wid);
     int k = 0;
-    for (; k + 2 < cnt; k += 2) {                        // peeled as gemv_dot4_kernel: no load under a condition
+    for (; k + 2 < cnt; k += 2) {                        // peeled and fenced as gemv_dot4_kernel
         load(1, wid + (k + 1) * nw);
+        __builtin_amdgcn_sched_barrier(0);               // the loads stay ahead of the use
         use(0);
         load(0, wid + (k + 2) * nw);
+        __builtin_amdgcn_sched_barrier(0);               // the loads stay ahead of the use
         use(1);
     }
     if (k + 1 < cnt) {
         load(1, wid + (k + 1) * nw);
+        __builtin_amdgcn_sched_barrier(0);               // the loads stay ahead of the use
         use(0);
         use(1);
     } else {
