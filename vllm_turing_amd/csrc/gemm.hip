@@ -1044,7 +1044,14 @@ __global__ void __launch_bounds__(256) stream_lds_kernel(const int8_t* __restric
     constexpr int STEP_BYTES = ROWS * 128;
     constexpr int LPS = ROWS / 8;                        // 1 KB loads per step
     extern __shared__ v4i ldsx[];
-    const int ks = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // The ring address of every direct-to-LDS load derives from the wavefront index and must be scalar (M0).  With the
+    // index from threadIdx the compiler wraps each load in a loop over the index's distinct values (one pass: it is
+    // uniform), which also spreads the step's loads through the iteration; in a scalar register the loads go out
+    // together.  Same bits either way; measured (same box): the scalar form 48 rows x N 12288 32.05 -> 30.04 us,
+    // 64 rows x N 5120 x K 17408 38.2 -> 37.6, but decode M = 6 / 8 / 16 17.91 / 18.42 / 20.74 -> 18.13 / 18.94 /
+    // 21.53 us (M = 32 unchanged), so it is taken for MT >= 3 only.
+    const int ks = MT >= 3 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int n0 = blockIdx.x * WR;
     uint8_t* const ring = reinterpret_cast<uint8_t*>(ldsx) + ks * NS * STEP_BYTES;
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a, (long)M * K), rsw = make_rsrc(w, (long)N * K);
@@ -1187,7 +1194,10 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const uint16_t* __restrict__
                                                     const int* __restrict__ rows) {
     constexpr int KS = 4, STEP_BYTES = RT * 16 * 128, LPS = 2 * RT;   // RT 16-row tiles share each activation load
     extern __shared__ v4i ldsx[];
-    const int ks = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wavefront index in a scalar register: the ring address of every direct-to-LDS load derives from it and must be
+    // scalar (M0); taken from threadIdx it made the compiler wrap each load in a loop over the index's values (N 248320,
+    // K 5120: M = 4 221.5 -> 216.7 us, M = 16 290.2 -> 288.2, same bits)
+    const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int n0 = blockIdx.x * 16 * RT;
     uint8_t* const ring = reinterpret_cast<uint8_t*>(ldsx) + ks * NS * STEP_BYTES;
     const __amdgpu_buffer_rsrc_t rsw = make_rsrc(w, (long)w_rows * K);
