@@ -165,8 +165,8 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
             bb[buf][r] = EPI == EPI_SMALL || EPI == EPI_LARGE_BIAS ? gload<uint16_t>(bias ? bias + n : &g_zero16) : 0;
         }
     };
-    auto finish = [&](int buf, int n0) {
-        int acc[R][M];
+    // the int32 sums of the row group in buffer buf against every activation row, reduced over the wavefront
+    auto sums = [&](int buf, int (&acc)[R][M]) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -181,6 +181,10 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
                 }
                 acc[r][m] = wave_sum(s);
             }
+    };
+    auto finish = [&](int buf, int n0) {
+        int acc[R][M];
+        sums(buf, acc);
         if constexpr (SILU) {                            // lane m writes out[m, n0]
 #pragma unroll
             for (int m = 0; m < M; ++m)
@@ -293,20 +297,7 @@ __global__ void __launch_bounds__(256) gemv_dot4_kernel(const int8_t* __restrict
         // the value lane r * M + m stores for output (m, n0 + r * nw) of the group in buffer buf
         auto value = [&](int buf) {
             int acc[R][M];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    int sum = 0;
-#pragma unroll
-                    for (int j = 0; j < CH; ++j) {
-                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].x, av[m][j].x, sum, false);
-                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].y, av[m][j].y, sum, false);
-                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].z, av[m][j].z, sum, false);
-                        sum = __builtin_amdgcn_sdot4(wb[buf][r][j].w, av[m][j].w, sum, false);
-                    }
-                    acc[r][m] = wave_sum(sum);
-                }
+            sums(buf, acc);
             uint32_t v = 0;
 #pragma unroll
             for (int r = 0; r < R; ++r)
