@@ -72,7 +72,9 @@ def test_argument_validation_codes(L):
     # 64-row tiles over more than 12288 weight rows: two K pieces where they fit two per CU (256 CUs), 16 KB each
     assert L.w8a8_scaled_mm_ws_size(64, 16384, 5120) == 4096 + 256 * 2 * 16384
     assert L.w8a8_scaled_mm_ws_size(33, 17408, 5120) == 4096 + 272 * 2 * 16384
-    assert L.w8a8_scaled_mm_ws_size(64, 24576, 5120) == 0       # 384 tiles: more than two per CU already
+    assert L.w8a8_scaled_mm_ws_size(64, 20480, 5120) == 4096 + 320 * 2 * 16384     # 5/4 tiles per CU
+    assert L.w8a8_scaled_mm_ws_size(64, 20544, 5120) == 0       # 321 tiles: past 5/4 per CU
+    assert L.w8a8_scaled_mm_ws_size(64, 24576, 5120) == 0       # 384 tiles
     assert L.w8a8_scaled_mm_ws_size(96, 13312, 5120) == 0       # two tile rows: 416 tiles
     assert L.w8a8_scaled_mm_ws_size(64, 16384, 2048) == 0       # 16 stages: pieces of 8
     assert L.w8a8_scaled_mm_ws_size(32, 16384, 5120) == 0       # 32 rows run on the streaming kernel

@@ -714,7 +714,9 @@ SPLIT_SHAPES = [
     (4096, 9472, 17408),    # 592 tiles: 256 whole in a launch of their own, 256 whole + 80 x 3 in the next
     (64, 16384, 5120),      # 64 x 64 tiles: 256 x 2 pieces
     (37, 13000, 5136),      # 204 x 2, ragged M and N, K % 128 = 16 (41 stages: pieces of 20 and 21)
-    (33, 17408, 17408),     # 272 x 2 at 68 stages
+    (33, 17408, 17408),     # 272 tiles at 136 stages: 240 as halves of 68, 32 as 110 + 26
+    (64, 20480, 5120),      # 320 tiles: 192 as halves of 20, 128 as 32 + 8
+    (40, 19000, 5136),      # 297 tiles, ragged M and N, 41 stages: 215 as 20 + 21, 82 as 33 + 8
 ]
 
 
@@ -760,7 +762,9 @@ def test_split_i32(L, M, N, K):
                                                 (1000, 3000, 17424, torch.float16, False),
                                                 (1536, 14336, 17408, torch.float16, True),
                                                 (48, 13312, 5120, torch.bfloat16, True),
-                                                (64, 17408, 5120, torch.float16, False)])
+                                                (64, 17408, 5120, torch.float16, False),
+                                                (40, 19000, 5136, torch.bfloat16, True),
+                                                (64, 20480, 5120, torch.float16, True)])
 def test_split_bits(L, M, N, K, dt, with_bias):
     """16-bit outputs of the split path bit-identical to w8a8_scaled_mm's (no workspace) and to the oracle's large-M
     epilogue of the exact products."""
@@ -793,7 +797,7 @@ def test_split_shared_workspace_and_graph(L):
     """One workspace for calls of different shapes in a row, then the split path captured in a HIP graph and replayed
     three times with eager work in between: every result equal to the eager one."""
     say("split shared workspace + graph replay")
-    shapes = [(1000, 3000, 17424), (64, 16384, 5120), (300, 1000, 17408), (1000, 3000, 17424)]
+    shapes = [(1000, 3000, 17424), (64, 16384, 5120), (300, 1000, 17408), (64, 20480, 5120), (1000, 3000, 17424)]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     ws = torch.zeros(4096 + cus * 262144, dtype=torch.uint8, device=DEV)
     g = torch.Generator().manual_seed(5)

@@ -25,9 +25,10 @@ def bits(t):
 def test_noalloc_matches_workspace_entry(L):
     st = torch.cuda.current_stream().cuda_stream
     g = torch.Generator().manual_seed(11)
-    # three calls in a row, each with a smaller input; all split over K (M=4096, N=5120, K=17408: 256 whole tiles
-    # + 64 x 4 pieces, every slot of the scratch; M=512: 96 x 2 pieces; M=64: 256 64 x 64 tiles x 2 pieces)
-    for M, N, K in ((4096, 5120, 17408), (512, 12288, 5120), (64, 16384, 5120)):
+    # four calls in a row, each with a smaller input; all split over K (M=4096, N=5120, K=17408: 256 whole tiles
+    # + 64 x 4 pieces, every slot of the scratch; M=40: 297 64 x 64 tiles x 2 pieces, 82 of them uneven; M=64: 256
+    # 64 x 64 tiles x 2 pieces; M=512: 96 x 2 pieces)
+    for M, N, K in ((4096, 5120, 17408), (40, 19000, 5136), (64, 16384, 5120), (512, 12288, 5120)):
         print(f"noalloc M={M} N={N} K={K}", flush=True)
         need = L.w8a8_scaled_mm_ws_size(M, N, K)
         assert need > 4096

@@ -620,7 +620,8 @@ __device__ __forceinline__ bool split_exchange(v16i (&acc)[FM][FN], int* ws, int
 // KSPLIT (the mid configurations, `splits` K pieces): the grid is every BM x BN tile of the output times `splits`;
 // workgroup u (after the XCD remap) runs piece u / T of tile u % T (T tiles, column-major over the BM-row tile rows, so
 // that the tile rows of one weight column and the workgroups of one K range sit on one XCD) and meets the other pieces
-// in the workspace `ws` (split_exchange).
+// in the workspace `ws` (split_exchange); t_base > 0 there selects the uneven two-piece form for the last t_base
+// tiles (dispatch order instead of the XCD remap, described where it is mapped).
 template <typename T, int EPI, int WM, int WN, int FM, int FN, int KB, int NS, int SPLIT = 0, bool LEAD = false,
           int GM = GROUP_M, bool PRIO = false, bool KSPLIT = false>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
@@ -645,12 +646,33 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const int8_t* __rest
     int m0, n0, kst0 = 0, nk = (K + KB - 1) / KB, piece = 0, rt = 0;   // tile origin, first stage and stage count
     if constexpr (KSPLIT) {
         const int TMb = (M + BM - 1) / BM, Tb = TMb * ((N + BN - 1) / BN);
-        piece = u / Tb;
-        rt = u % Tb;
+        if (t_base > 0) {
+            // uneven two-piece form (splits == 2; t_base = the number of uneven tiles, the last ones), in dispatch
+            // order: both halves of each even tile and the long first piece (stages [0, L)) of each uneven tile,
+            // which together fill one round of the grid's slots, then the uneven tiles' short pieces, which start on
+            // the slots the halves free.  L = h + 5/8 of the rest (32 of 40 stages): 4/8 balances a half and a
+            // short piece against a long one on paper; same box, M 64 x N 19456 / 20480 x K 5120, 3/8 32.4 / 34.2
+            // us, 4/8 31.9 / 32.8, 5/8 31.5 / 32.1, 6/8 31.4 / 32.1, all within 1% at 272 tiles
+            const int b = blockIdx.x, te = Tb - t_base, h = nk / 2, L = h + (nk - h) * 5 / 8;
+            if (b < 2 * te) {
+                rt = b >> 1;
+                piece = b & 1;
+            } else {
+                const int j = b - 2 * te;
+                piece = j >= t_base;
+                rt = te + j - piece * t_base;
+            }
+            const int cut = rt < te ? h : L;
+            kst0 = piece ? cut : 0;
+            nk = piece ? nk - cut : cut;
+        } else {
+            piece = u / Tb;
+            rt = u % Tb;
+            kst0 = piece * nk / splits;
+            nk = (piece + 1) * nk / splits - kst0;       // >= 1: the host takes splits <= the stage count
+        }
         m0 = (rt % TMb) * BM;
         n0 = (rt / TMb) * BN;
-        kst0 = piece * nk / splits;
-        nk = (piece + 1) * nk / splits - kst0;           // >= 1: the host takes splits <= the stage count
     } else {
         const int TM = (M + SUPER - 1) / SUPER, TN = (N + SUPER - 1) / SUPER;
         const int t = t_base + u / SUB, q = u % SUB;
@@ -1839,20 +1861,31 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
 // to 17% below, four to eight lose more; more tiles than that lose (M 64 x N 24576 36.4 -> 41.0, M 128 x N 17408
 // 42.3 -> 45.1), and 3 K stages (three workgroups per CU) run the unsplit tiles 40% slower and the split ones no
 // faster.
+// More tiles than CUs: 2 (tiles - CUs) of them split unevenly (gemm_kernel's KSPLIT mapping), so that the first round
+// of two workgroups per CU holds both halves of the others and a long first piece of these, and their short pieces
+// run on the slots the halves free; that takes the split up to 5/4 tiles per CU.  Same box, equal halves -> uneven:
+// M 64 x N 17408 x K 5120 (272 tiles) 32.6 -> 29.8 us, M 33 x N 17408 28.9 -> 26.7, M 40 x N 17408 x K 17408
+// 75.5 -> 72.8; unsplit -> uneven: M 64 x N 20480 (320 tiles) 35.5 -> 32.1; past 5/4 it loses (M 48 x N 22528, 352
+// tiles, 33.5 -> 34.0; M 64 x N 24576 37.1 -> 37.9).
 #ifndef W8_MID_SPLIT
 #define W8_MID_SPLIT -1                                  // -1: mid_split_plan's choice; 0 or 1: none; s >= 2: s pieces
 #endif
+#ifndef W8_MID_UNEVEN
+#define W8_MID_UNEVEN 1                                  // 0: equal halves only, up to 17/16 tiles per CU
+#endif
 static bool mid64_path(int M, int N) { return M > 32 && M <= MID_GEMM_MAX_M && N > MID_GEMM_WIDE_N; }
-static int mid_split_plan(int M, int N, int K, int cus, long* bytes) {
+static int mid_split_plan(int M, int N, int K, int cus, long* bytes, int* uneven = nullptr) {
     *bytes = 0;
+    if (uneven) *uneven = 0;
     if (!mid64_path(M, N)) return 1;
     const int tiles = ((M + 63) / 64) * ((N + 63) / 64), nk = (K + 127) / 128;
     int s = W8_MID_SPLIT;
     // two pieces where they fit two workgroups per CU in about one round (64 KB of LDS each) and stay >= 16 stages
-    if (s < 0) s = 16 * tiles <= 17 * cus && nk >= 32 ? 2 : 1;
+    if (s < 0) s = (W8_MID_UNEVEN ? 4 * tiles <= 5 * cus : 16 * tiles <= 17 * cus) && nk >= 32 ? 2 : 1;
     // at most 4096 slots of 16 KB, so that any plan fits the allocation-free entry's scratch (64 MiB of slots)
     s = min(min(s, nk), 4096 / tiles);
     if (s < 2 || tiles > SPLIT_HEAD_INTS) return 1;
+    if (uneven && W8_MID_UNEVEN && s == 2 && tiles > cus) *uneven = min(2 * (tiles - cus), tiles);
     *bytes = (long)SPLIT_HEAD_INTS * 4 + (long)tiles * s * 64 * 64 * 4;
     return s;
 }
@@ -1861,10 +1894,11 @@ template <typename T, int EPI>
 static void launch_gemm(const Args& p, int policy = W8_GEMM_POLICY) {
     if (policy == 1 && p.ws) {                           // the K splits, when the caller gave a workspace
         long mbytes;
-        const int ms = mid_split_plan(p.M, p.N, p.K, cu_count(), &mbytes);
+        int uneven;
+        const int ms = mid_split_plan(p.M, p.N, p.K, cu_count(), &mbytes, &uneven);
         if (ms >= 2 && mbytes <= p.ws_bytes) {
             const int tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
-            launch_gemm_cfg<T, EPI, Mid64Cfg, true>(p, 0, tiles * ms, ms);
+            launch_gemm_cfg<T, EPI, Mid64Cfg, true>(p, uneven, tiles * ms, ms);
             return;
         }
         int full, rem;
