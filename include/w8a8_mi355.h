@@ -67,9 +67,10 @@ int w8a8_scaled_mm(const void* a, const void* w, const void* sa, const void* sw,
 
 /* w8a8_scaled_mm (and so w8a8_big, which is its no-bias per-row / per-column case) with a caller workspace for the
  * prefill GEMM's K splits: when the 256 x 256 super tiles leave a last partial round of at most half the CUs, each of
- * those tiles runs as 2..8 K pieces (at least 3 after whole rounds), and 33..64 rows against more than 12288 weight
- * rows run their 64 x 64 tiles as 2 K pieces of at least 16 stages where the tiles number at most 5/4 of the CUs
- * (up to 20480 weight rows on 256 CUs; past one tile per CU some tiles' pieces are of unequal length); the pieces'
+ * those tiles runs as 2..8 K pieces (at least 3 after whole rounds), and 33..128 rows run their 64 x 64 tiles as K
+ * pieces of at least 16 stages: against more than 12288 weight rows 2 pieces where the tiles number at most 5/4 of
+ * the CUs (up to 20480 weight rows at 64 rows on 256 CUs; past one tile per CU some tiles' pieces are of unequal
+ * length), against fewer (more than 4096, or K of at least 8192) as many as fill two workgroups per CU; the pieces'
  * int32 partial sums meet in the workspace (the last piece to finish adds them and runs the epilogue; the results
  * are bit-identical to w8a8_scaled_mm's).  workspace: 16-byte aligned,
  * ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K) (it may be null when that is 0); its first 4 KB (tile counters) must be

@@ -78,6 +78,12 @@ def test_argument_validation_codes(L):
     assert L.w8a8_scaled_mm_ws_size(96, 13312, 5120) == 0       # two tile rows: 416 tiles
     assert L.w8a8_scaled_mm_ws_size(64, 16384, 2048) == 0       # 16 stages: pieces of 8
     assert L.w8a8_scaled_mm_ws_size(32, 16384, 5120) == 0       # 32 rows run on the streaming kernel
+    # at most 12288 weight rows: as many pieces as fill two workgroups per CU, where N > 4096 or K >= 64 stages
+    assert L.w8a8_scaled_mm_ws_size(64, 12288, 5120) == 4096 + 192 * 2 * 16384
+    assert L.w8a8_scaled_mm_ws_size(128, 5120, 17408) == 4096 + 160 * 3 * 16384
+    assert L.w8a8_scaled_mm_ws_size(64, 1024, 17408) == 4096 + 16 * 8 * 16384
+    assert L.w8a8_scaled_mm_ws_size(64, 4096, 5120) == 0        # 40 stages, N <= 4096
+    assert L.w8a8_scaled_mm_ws_size(128, 12288, 5120) == 0      # 384 tiles: one piece each
     # w8a8_gemv_silu: -1 on bad arguments, 1 where the VALU GEMV does not take M or K
     assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 0, 5120, 1, 1, 0, None) == -1      # I < 1
     assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 64, 40, 1, 1, 0, None) == -1      # K % 16

@@ -717,6 +717,10 @@ SPLIT_SHAPES = [
     (33, 17408, 17408),     # 272 tiles at 136 stages: 240 as halves of 68, 32 as 110 + 26
     (64, 20480, 5120),      # 320 tiles: 192 as halves of 20, 128 as 32 + 8
     (40, 19000, 5136),      # 297 tiles, ragged M and N, 41 stages: 215 as 20 + 21, 82 as 33 + 8
+    (64, 12288, 5120),      # 192 64 x 64 tiles x 2 pieces
+    (128, 5120, 17408),     # 160 tiles (two tile rows) x 3 pieces
+    (100, 1000, 17424),     # 32 tiles x 8 pieces, ragged M, N and K (137 stages)
+    (40, 6000, 5136),       # 94 tiles x 2, ragged N and K
 ]
 
 
@@ -764,7 +768,9 @@ def test_split_i32(L, M, N, K):
                                                 (48, 13312, 5120, torch.bfloat16, True),
                                                 (64, 17408, 5120, torch.float16, False),
                                                 (40, 19000, 5136, torch.bfloat16, True),
-                                                (64, 20480, 5120, torch.float16, True)])
+                                                (64, 20480, 5120, torch.float16, True),
+                                                (128, 5120, 17408, torch.bfloat16, True),
+                                                (72, 8000, 5120, torch.float16, False)])
 def test_split_bits(L, M, N, K, dt, with_bias):
     """16-bit outputs of the split path bit-identical to w8a8_scaled_mm's (no workspace) and to the oracle's large-M
     epilogue of the exact products."""

@@ -1852,9 +1852,9 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
     return s;
 }
 
-// K split of the 64 x 64 mid tiles (33..64 rows against more than 12288 weight rows).  A workgroup of those tiles is
-// bound by its own stage loop rather than by HBM (at M = 64, K = 5120 the time grows ~20 us + bytes / 8.8 TB/s with
-// N), so two K pieces per tile halve each workgroup's loop where both pieces of every tile fit at two workgroups per
+// K split of the 64 x 64 mid tiles (33..128 rows, with a workspace).  Against more than 12288 weight rows a workgroup
+// is bound by its own stage loop rather than by HBM (at M = 64, K = 5120 the time grows ~20 us + bytes / 8.8 TB/s
+// with N), so two K pieces per tile halve each workgroup's loop where both pieces of every tile fit at two workgroups per
 // CU (64 KB of LDS each).  Same box, rotated weights, bf16 with bias, unsplit -> split: M 64 x N 16384 34.0 -> 25.2 us,
 // M 64 x N 12800 33.6 -> 23.8, M 48 x N 13312 30.8 -> 22.8, M 64 x N 13312 x K 17408 93.1 -> 59.8, M 64 x N 17408
 // (272 tiles) 35.1 -> 32.1, M 40 x N 17408 x K 17408 85.4 -> 76.0; three pieces tie with two at 272 tiles and lose up
@@ -1873,14 +1873,29 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
 #ifndef W8_MID_UNEVEN
 #define W8_MID_UNEVEN 1                                  // 0: equal halves only, up to 17/16 tiles per CU
 #endif
-static bool mid64_path(int M, int N) { return M > 32 && M <= MID_GEMM_MAX_M && N > MID_GEMM_WIDE_N; }
+// At most 12288 weight rows (where, without a workspace, the streaming passes or the 64 x 128 tiles run): as many
+// pieces per tile as fill two workgroups per CU once, min(2 CUs / tiles, stages / 16, 8), where N > 4096 or K has at
+// least 64 stages.  Same box, rotated weights, bf16 with bias, without -> with the split: M 64 x N 12288 x K 5120
+// 33.7 -> 24.7 us, M 33 x N 12288 27.3 -> 21.4, M 64 x N 10240 32.5 -> 23.7, M 64 x N 8192 18.3 -> 15.6, M 40 x
+// N 6144 14.7 -> 13.7, M 64 x N 5120 x K 5120 17.2 -> 14.4, M 64 x N 5120 x K 17408 37.8 -> 31.0, M 48 x N 6144 x
+// K 17408 34.0 -> 31.8, M 64 x N 1024 x K 17408 26.0 -> 20.1, M 64 x N 6144 x K 4096 14.8 -> 11.9; at 65..128 rows,
+// where the streaming passes read the weights twice, M 128 x N 5120 x K 17408 74.9 -> 37.2, M 96 64.5 -> 34.1,
+// M 128 x N 8192 x K 5120 35.4 -> 21.4, M 128 x N 6144 34.8 -> 20.6, M 100 x N 5120 x K 5120 31.2 -> 18.8.  At
+// N <= 4096 with fewer stages the streaming passes stay faster (M 64 x N 4096 x K 5120 12.0 against 13.5, N 2048
+// 11.3 against 12.9, M 48 x N 3072 10.7 against 12.7); M 128 x N 12288 (384 tiles) gets one piece and keeps the
+// 64 x 128 tiles (26.8 us either way).
+static bool mid64_path(int M, int N, int K) {
+    return M > 32 && M <= MID_GEMM_MAX_M && (N > 4096 || (K + 127) / 128 >= 64);
+}
 static int mid_split_plan(int M, int N, int K, int cus, long* bytes, int* uneven = nullptr) {
     *bytes = 0;
     if (uneven) *uneven = 0;
-    if (!mid64_path(M, N)) return 1;
+    if (!mid64_path(M, N, K)) return 1;
     const int tiles = ((M + 63) / 64) * ((N + 63) / 64), nk = (K + 127) / 128;
     int s = W8_MID_SPLIT;
-    // two pieces where they fit two workgroups per CU in about one round (64 KB of LDS each) and stay >= 16 stages
+    if (s < 0 && N <= MID_GEMM_WIDE_N) s = min(min(2 * cus / tiles, nk / 16), SPLIT_MAX);
+    // wider: two pieces where they fit two workgroups per CU in about one round (64 KB of LDS each) and stay >= 16
+    // stages
     if (s < 0) s = (W8_MID_UNEVEN ? 4 * tiles <= 5 * cus : 16 * tiles <= 17 * cus) && nk >= 32 ? 2 : 1;
     // at most 4096 slots of 16 KB, so that any plan fits the allocation-free entry's scratch (64 MiB of slots)
     s = min(min(s, nk), 4096 / tiles);
