@@ -70,11 +70,12 @@ int w8a8_scaled_mm(const void* a, const void* w, const void* sa, const void* sw,
  * those tiles runs as 2..8 K pieces (at least 3 after whole rounds), and 33..128 rows run their 64 x 64 tiles as K
  * pieces of at least 16 stages: against more than 12288 weight rows 2 pieces where the tiles number at most 5/4 of
  * the CUs (up to 20480 weight rows at 64 rows on 256 CUs; past one tile per CU some tiles' pieces are of unequal
- * length), against fewer (more than 4096, or K of at least 8192) as many as fill two workgroups per CU; the pieces'
- * int32 partial sums meet in the workspace (the last piece to finish adds them and runs the epilogue; the results
- * are bit-identical to w8a8_scaled_mm's).  workspace: 16-byte aligned,
- * ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K) (it may be null when that is 0); its first 4 KB (tile counters) must be
- * zero before the first call, and every call leaves them zero.  Calls that share a workspace must not overlap.
+ * length), against fewer (more than 4096, or K of at least 8192) as many as fill two workgroups per CU, as do
+ * 129..256 rows against at most 8192 weight rows with K of at least 8192; the pieces' int32 partial sums meet in the
+ * workspace (the last piece to finish adds them and runs the epilogue; the results are bit-identical to
+ * w8a8_scaled_mm's).  workspace: 16-byte aligned, ws_bytes >= w8a8_scaled_mm_ws_size(M, N, K) (it may be null when
+ * that is 0); its first 4 KB (tile counters) must be zero before the first call, and every call leaves them zero.
+ * Calls that share a workspace must not overlap.
  * dtype 2 writes the raw int32 accumulators acc [M, N] to out (sa, sw, bias unused; for checking).  Returns -1 on bad
  * arguments (a missing or too small workspace included), else the HIP error code of the launches.
  * No counterpart in the reference, whose w8a8_big rejects a workspace (vllm_turing/csrc/w8a8_big.cu:57-59); this

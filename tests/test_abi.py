@@ -84,6 +84,9 @@ def test_argument_validation_codes(L):
     assert L.w8a8_scaled_mm_ws_size(64, 1024, 17408) == 4096 + 16 * 8 * 16384
     assert L.w8a8_scaled_mm_ws_size(64, 4096, 5120) == 0        # 40 stages, N <= 4096
     assert L.w8a8_scaled_mm_ws_size(128, 12288, 5120) == 0      # 384 tiles: one piece each
+    assert L.w8a8_scaled_mm_ws_size(192, 5120, 17408) == 4096 + 240 * 2 * 16384     # 129..256 rows, K >= 64 stages
+    assert L.w8a8_scaled_mm_ws_size(256, 5120, 5120) == 0       # 129..256 rows at 40 stages
+    assert L.w8a8_scaled_mm_ws_size(256, 5120, 17408) == 0      # 320 tiles: one piece each
     # w8a8_gemv_silu: -1 on bad arguments, 1 where the VALU GEMV does not take M or K
     assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 0, 5120, 1, 1, 0, None) == -1      # I < 1
     assert L.w8a8_gemv_silu(16, 16, 0, 0, None, 16, 1, 64, 40, 1, 1, 0, None) == -1      # K % 16

@@ -721,6 +721,8 @@ SPLIT_SHAPES = [
     (128, 5120, 17408),     # 160 tiles (two tile rows) x 3 pieces
     (100, 1000, 17424),     # 32 tiles x 8 pieces, ragged M, N and K (137 stages)
     (40, 6000, 5136),       # 94 tiles x 2, ragged N and K
+    (192, 5120, 17408),     # three tile rows: 240 tiles x 2
+    (150, 4000, 17424),     # 189 tiles x 2, ragged M, N and K
 ]
 
 
@@ -770,7 +772,8 @@ def test_split_i32(L, M, N, K):
                                                 (40, 19000, 5136, torch.bfloat16, True),
                                                 (64, 20480, 5120, torch.float16, True),
                                                 (128, 5120, 17408, torch.bfloat16, True),
-                                                (72, 8000, 5120, torch.float16, False)])
+                                                (72, 8000, 5120, torch.float16, False),
+                                                (160, 5120, 17408, torch.bfloat16, True)])
 def test_split_bits(L, M, N, K, dt, with_bias):
     """16-bit outputs of the split path bit-identical to w8a8_scaled_mm's (no workspace) and to the oracle's large-M
     epilogue of the exact products."""

@@ -1795,7 +1795,8 @@ static void launch_gemm_cfg(const Args& p, int t_base, int blocks, int splits = 
 // kernel: N = 5120, K = 17408, M = 33..64 114 -> 35-38 us, M = 96 113 -> 65 us, M = 128 114 -> 76 us; N = 12288,
 // K = 5120, M = 33..64 42-45 -> 31-35 us; N = 8192, M = 128 38 -> 36 us.  Past these bounds the prefill kernel is
 // faster (N = 12288, M = 128: 50 against 69 us; N = 17408, M = 33: 46 against 51 us): the passes re-read the weights
-// and the 64-row rings leave few wavefronts per CU.
+// and the 64-row rings leave few wavefronts per CU.  With a workspace the 64 x 64 tiles split over K take most of
+// these shapes (mid_split_plan).
 static bool mid_stream(int M, int N) { return (M <= 64 && N <= 12288) || (M <= 128 && N <= 8192); }
 template <typename T, int EPI>
 static void launch_stream_rows(const Args& p) {
@@ -1852,7 +1853,7 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
     return s;
 }
 
-// K split of the 64 x 64 mid tiles (33..128 rows, with a workspace).  Against more than 12288 weight rows a workgroup
+// K split of the 64 x 64 mid tiles (33..256 rows, with a workspace).  Against more than 12288 weight rows a workgroup
 // is bound by its own stage loop rather than by HBM (at M = 64, K = 5120 the time grows ~20 us + bytes / 8.8 TB/s
 // with N), so two K pieces per tile halve each workgroup's loop where both pieces of every tile fit at two workgroups per
 // CU (64 KB of LDS each).  Same box, rotated weights, bf16 with bias, unsplit -> split: M 64 x N 16384 34.0 -> 25.2 us,
@@ -1884,8 +1885,16 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
 // N <= 4096 with fewer stages the streaming passes stay faster (M 64 x N 4096 x K 5120 12.0 against 13.5, N 2048
 // 11.3 against 12.9, M 48 x N 3072 10.7 against 12.7); M 128 x N 12288 (384 tiles) gets one piece and keeps the
 // 64 x 128 tiles (26.8 us either way).
+// 129..256 rows against at most 8192 weight rows (the 64 x 128 tiles' range above 128 rows) split the same way where
+// K has at least 64 stages: M 192 x N 5120 x K 17408 65.3 -> 46.5 us, M 160 60.4 -> 44.5, M 256 x N 4096 x K 17408
+// 63.8 -> 45.3; with 40 stages they lose (M 256 x N 5120 x K 5120 24.2 against 25.7, M 160 x N 6144 23.5 against
+// 24.4), and two uneven pieces past one tile per CU tie or lose here (M 256 x N 5120 x K 17408 64.9 / 64.5, M 128 x
+// N 10240 x K 5120 26.7 / 27.5).
 static bool mid64_path(int M, int N, int K) {
-    return M > 32 && M <= MID_GEMM_MAX_M && (N > 4096 || (K + 127) / 128 >= 64);
+    const int nk = (K + 127) / 128;
+    if (M <= 32) return false;
+    if (M <= MID_GEMM_MAX_M) return N > 4096 || nk >= 64;
+    return M <= 2 * MID_GEMM_MAX_M && N <= 8192 && nk >= 64;
 }
 static int mid_split_plan(int M, int N, int K, int cus, long* bytes, int* uneven = nullptr) {
     *bytes = 0;
