@@ -1854,14 +1854,13 @@ static int split_plan(int M, int N, int K, int cus, int* full, int* rem, long* b
 }
 
 // K split of the 64 x 64 mid tiles (33..256 rows, with a workspace).  Against more than 12288 weight rows a workgroup
-// is bound by its own stage loop rather than by HBM (at M = 64, K = 5120 the time grows ~20 us + bytes / 8.8 TB/s
-// with N), so two K pieces per tile halve each workgroup's loop where both pieces of every tile fit at two workgroups per
-// CU (64 KB of LDS each).  Same box, rotated weights, bf16 with bias, unsplit -> split: M 64 x N 16384 34.0 -> 25.2 us,
-// M 64 x N 12800 33.6 -> 23.8, M 48 x N 13312 30.8 -> 22.8, M 64 x N 13312 x K 17408 93.1 -> 59.8, M 64 x N 17408
-// (272 tiles) 35.1 -> 32.1, M 40 x N 17408 x K 17408 85.4 -> 76.0; three pieces tie with two at 272 tiles and lose up
-// to 17% below, four to eight lose more; more tiles than that lose (M 64 x N 24576 36.4 -> 41.0, M 128 x N 17408
-// 42.3 -> 45.1), and 3 K stages (three workgroups per CU) run the unsplit tiles 40% slower and the split ones no
-// faster.
+// is bound by its own stage loop rather than by HBM (at M = 64, K = 5120 the time grows ~20 us + bytes / 8.8 TB/s with
+// N), so two K pieces per tile halve each workgroup's loop where both pieces of every tile fit at two workgroups per CU
+// (64 KB of LDS each).  Same box, rotated weights, bf16 with bias, unsplit -> split: M 64 x N 16384 34.0 -> 25.2 us, M
+// 64 x N 12800 33.6 -> 23.8, M 48 x N 13312 30.8 -> 22.8, M 64 x N 13312 x K 17408 93.1 -> 59.8, M 64 x N 17408 (272
+// tiles) 35.1 -> 32.1, M 40 x N 17408 x K 17408 85.4 -> 76.0; three pieces tie with two at 272 tiles and lose up to 17%
+// below, four to eight lose more; more tiles than that lose (M 64 x N 24576 36.4 -> 41.0, M 128 x N 17408 42.3 ->
+// 45.1), and 3 K stages (three workgroups per CU) run the unsplit tiles 40% slower and the split ones no faster.
 // More tiles than CUs: 2 (tiles - CUs) of them split unevenly (gemm_kernel's KSPLIT mapping), so that the first round
 // of two workgroups per CU holds both halves of the others and a long first piece of these, and their short pieces
 // run on the slots the halves free; that takes the split up to 5/4 tiles per CU.  Same box, equal halves -> uneven:
