@@ -10,6 +10,8 @@ is GPU work only (HIP events on the launch stream, bracketed by synchronizations
 Also reported:
   decode_other_m: the same weights at M = 2, 4, 8, 16, 32, 64 through the entry the reference dispatches at that M
     (GEMV up to 12 rows, the mid-band MMA up to 32, the large-M GEMM above);
+  batched_decode_split: M = 64 / 128 rows against N 12288 x K 5120 and N 5120 x K 17408 through the workspace entry
+    (64 x 64 tiles split over K), with the same entry's time without a workspace beside it;
   gemm: prefill GEMM at M=4096, K=5120, N=12288 with bias, bf16 out, five weight copies rotated per launch (the
     weights come from HBM), in TOPS of 2*M*N*K ops (MFMA-bound roofline),
     timed after a 2 s untimed run of it that samples the median gfx clock amd-smi reports (sclk_mhz) and settles
@@ -505,6 +507,38 @@ def bench_headline(torch, L, st, dev, args):
     print(f"[bench] GEMV M=2..64: {decode_m}", file=sys.stderr, flush=True)
     del ws
 
+    # batched decode on the other projections (fp16 out, no bias, rotated weights beyond the MALL): the workspace
+    # entry, whose 64 x 64 tiles split over K, beside the same entry without a workspace (the streaming passes of at
+    # most 64 rows); the two give the same bits (the GPU tests check that)
+    mid_split = {}
+    gen_m = torch.Generator(device=dev).manual_seed(23)
+    for (Mm, Nm, Km) in ((64, 12288, 5120), (64, 5120, 17408), (128, 5120, 17408)):
+        mcopies = max(2, int(4.0e8 // (Nm * Km)) + 1)
+        wm = [torch.randint(-127, 128, (Nm, Km), dtype=torch.int8, device=dev, generator=gen_m)
+              for _ in range(mcopies)]
+        am = torch.randint(-127, 128, (Mm, Km), dtype=torch.int8, device=dev, generator=gen_m)
+        sam = torch.rand(Mm, device=dev, generator=gen_m) * 1e-2
+        swm = torch.rand(Nm, device=dev, generator=gen_m) * 1e-3
+        outm = torch.empty(Mm, Nm, dtype=torch.float16, device=dev)
+
+        def split_on(i, Mm=Mm, Nm=Nm, Km=Km, wm=wm, am=am, sam=sam, swm=swm, outm=outm, mcopies=mcopies):
+            if scaled_mm_ws(L, st, am, wm[i % mcopies], sam, swm, None, outm, Mm, Nm, Km, 0) != 0:
+                raise RuntimeError(f"batched decode M={Mm} N={Nm} K={Km}: workspace entry failed")
+
+        def split_off(i, Mm=Mm, Nm=Nm, Km=Km, wm=wm, am=am, sam=sam, swm=swm, outm=outm, mcopies=mcopies):
+            if L.w8a8_scaled_mm(am.data_ptr(), wm[i % mcopies].data_ptr(), sam.data_ptr(), swm.data_ptr(), None,
+                                outm.data_ptr(), Mm, Nm, Km, 1, 1, 0, st()) != 0:
+                raise RuntimeError(f"batched decode M={Mm} N={Nm} K={Km}: entry failed")
+
+        ms_on, _ = graph_time(torch, split_on, 2 * mcopies, 200, 20)
+        ms_off, _ = graph_time(torch, split_off, 2 * mcopies, 200, 20)
+        b_m = Nm * Km + Mm * Km + 2 * Mm * Nm + 4 * Nm + 4 * Mm
+        mid_split[f"M{Mm}_N{Nm}_K{Km}"] = {"us": round(ms_on * 1e3, 2), "gbs": round(b_m / ms_on / 1e6, 1),
+                                           "frac": round(b_m / ms_on / 1e6 / HBM_PEAK_GBS, 4),
+                                           "us_without_workspace": round(ms_off * 1e3, 2)}
+        del wm
+    print(f"[bench] batched decode, K split: {mid_split}", file=sys.stderr, flush=True)
+
     # ---- prefill GEMM, M=4096, bias, bf16 ---------------------------------------------------------------------------
     Mg, Kg, Ng = 4096, workloads.HIDDEN, 12288
     p = workloads.prefill(Mg)
@@ -669,6 +703,10 @@ def bench_headline(torch, L, st, dev, args):
                                        f"dispatches at each M (w8a8_gemv <= 12, w8a8_mma <= 32, above w8a8_big's "
                                        f"kernels through the workspace entry, split over K where the plan splits)",
                            **decode_m},
+        "batched_decode_split": {"workload": "batched decode W8A8 on the other projections, fp16 out, rotated "
+                                             "weights: w8a8_scaled_mm_ws (64 x 64 tiles split over K) beside "
+                                             "w8a8_scaled_mm without a workspace (streaming passes of <= 64 rows)",
+                                 **mid_split},
         "gemm": {"workload": f"prefill W8A8 GEMM M={Mg} K={Kg} N={Ng}, bias, bf16 out, {gcopies} rotated weight copies "
                              f"({gcopies * Ng * Kg / 1e6:.0f} MB > 256 MB MALL)", "ms": round(ms_gemm, 4),
                  "launches": n_gemm, "tops": round(gemm_tops, 1),
